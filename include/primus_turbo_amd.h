@@ -1,0 +1,257 @@
+/*
+ * primus_turbo_amd.h -- C ABI of the MI355X (gfx950) FP8 linear-path library
+ * (libprimus_turbo_amd.so).
+ *
+ * Every entry point takes raw device pointers, int64 sizes, small integer
+ * type codes and a HIP stream (hipStream_t passed as void*).  The caller owns
+ * every buffer: outputs and workspaces are allocated by the caller (the
+ * library never allocates, frees or synchronises the host).  All work is
+ * enqueued on the given stream; nothing is read back to the host.  Each call
+ * returns PTA_OK or a negative error code; pta_last_error() returns a
+ * thread-local message describing the last failure.
+ *
+ * Each declaration names the reference interface it replaces (paths relative
+ * to the Primus-Turbo repository root).  The reference's native ops are
+ * TORCH_LIBRARY schemas (csrc/pytorch/bindings_pytorch.cpp:13-130) that
+ * allocate their outputs with at::empty; here the equivalent Python layer
+ * allocates and passes pointers in.
+ */
+#ifndef PRIMUS_TURBO_AMD_H
+#define PRIMUS_TURBO_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+#define PTA_OK 0
+#define PTA_ERR_INVALID_ARG (-1)
+#define PTA_ERR_HIP (-2)
+#define PTA_ERR_UNSUPPORTED (-3)
+
+/* ---- element type codes ---------------------------------------------------- */
+#define PTA_F32 0
+#define PTA_F16 1
+#define PTA_BF16 2
+
+/* ---- fp8 formats (OCP, gfx950) --------------------------------------------- */
+#define PTA_E4M3 0 /* torch.float8_e4m3fn, max 448   */
+#define PTA_E5M2 1 /* torch.float8_e5m2,   max 57344 */
+
+/* ---- scaling granularity: values equal ScalingGranularity.<X>.value --------
+ * (primus_turbo/pytorch/core/low_precision.py:125-133, enum auto() from 1) */
+#define PTA_TENSORWISE 1
+#define PTA_ROWWISE 2
+#define PTA_BLOCKWISE 3
+#define PTA_MX_BLOCKWISE 4
+
+typedef void *pta_stream_t; /* hipStream_t */
+
+/* Thread-local description of the last error (empty string if none). */
+const char *pta_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int pta_abi_version(void);
+
+/* ============================================================================
+ * Quantization
+ * ========================================================================== */
+
+/* Workspace bytes needed by pta_quantize_fp8_tensorwise for n elements. */
+size_t pta_quantize_fp8_tensorwise_workspace_size(int64_t n);
+
+/* Tensorwise: amax = max|x| (NaN ignored), scale = fp8_max / max(amax, 1e-12),
+ * q = fp8(clamp(x * scale)), *scale_inv = 1 / scale.  If scale is non-NULL it
+ * is a device scalar used instead of the amax-derived one.
+ * Replaces quantize_fp8_tensorwise (csrc/pytorch/quantization/quantization.cpp:42-88). */
+int pta_quantize_fp8_tensorwise(const void *x, int in_dtype, int64_t n, const float *scale,
+                                void *q, int fmt, float *scale_inv, void *workspace,
+                                size_t workspace_bytes, pta_stream_t stream);
+
+/* Workspace bytes needed by pta_quantize_fp8_rowwise. */
+size_t pta_quantize_fp8_rowwise_workspace_size(int64_t outer, int64_t len, int64_t inner);
+
+/* Rowwise: x viewed as [outer, len, inner]; one scale per (outer, inner) slice
+ * reduced over `len` (the quantization axis), eps 1e-12.  scale_inv has
+ * outer*inner entries.  If scale is non-NULL (outer*inner entries) it is used
+ * instead of the amax-derived one.
+ * Replaces quantize_fp8_rowwise (csrc/pytorch/quantization/quantization.cpp:108-206). */
+int pta_quantize_fp8_rowwise(const void *x, int in_dtype, int64_t outer, int64_t len,
+                             int64_t inner, const float *scale, void *q, int fmt, float *scale_inv,
+                             void *workspace, size_t workspace_bytes, pta_stream_t stream);
+
+/* Blockwise 1-D: axis 1 -> 1 x block along N, s[M, ceil(N/block)];
+ * axis 0 -> block x 1 along M, s[ceil(M/block), N]; eps 1e-4.
+ * Replaces quant_fp8_blockwise_impl
+ * (primus_turbo/pytorch/kernels/quantization/quantization_impl.py:74-118). */
+int pta_quantize_fp8_blockwise(const void *x, int in_dtype, int64_t M, int64_t N, int64_t block,
+                               int axis, void *q, float *s, int fmt, pta_stream_t stream);
+
+/* Blockwise dual (one read of x): row-scaled q_row[M,N] + s_row[M, ceil(N/block)]
+ * and col-scaled q_col + s_col[ceil(M/block), N].  col_transposed = 0 writes
+ * q_col as [M, N] (the reference layout); 1 writes it as [N, M_pad] with
+ * M_pad = roundup(M, 128) and zero padding (K-contiguous operand for the NT
+ * wgrad GEMM).  Either output pair may be NULL.
+ * Replaces quant_fp8_blockwise_dual_impl (quantization_impl.py:229-274). */
+int pta_quantize_fp8_blockwise_dual(const void *x, int in_dtype, int64_t M, int64_t N,
+                                    int64_t block, void *q_row, float *s_row, void *q_col,
+                                    float *s_col, int col_transposed, int fmt, pta_stream_t stream);
+
+/* Blockwise 2-D weight quant: w[B, M, N] -> q[B, M, N],
+ * s[B, ceil(M/block), ceil(N/block)], one scale per block x block tile.
+ * If q_t is non-NULL the same bytes are also written transposed as
+ * [B, N, M_pad], M_pad = roundup(M, 128), padding bytes zero.
+ * Replaces quantize_fp8_blockwise_for_weight (quantization.cpp:1442-1476). */
+int pta_quantize_fp8_blockwise_for_weight(const void *w, int in_dtype, int64_t B, int64_t M,
+                                          int64_t N, int64_t block, void *q, float *s, void *q_t,
+                                          int fmt, pta_stream_t stream);
+
+/* Grouped segment row + col quant (block 128): rows of x[M, N] belong to G
+ * groups (group_offs[G+1], device).  Produces q_row[M,N], s_row_t[ceil(N/128), M]
+ * (transposed row scales), the 128-padded column-quantized q_col_pad[M+G*128, N]
+ * with s_col_pad[ceil((M+G*128)/128), N], and vk_lens[G] / vk_offs[G+1]
+ * (group lengths rounded up to 128 and their prefix sum).  All on device.
+ * Replaces quantize_fp8_blockwise_segment_m_row_col (quantization.cpp:1382-1439). */
+int pta_quantize_fp8_blockwise_segment_m_row_col(const void *x, int in_dtype, int64_t M,
+                                                 int64_t N, int64_t G, const int64_t *group_lens,
+                                                 const int64_t *group_offs, int64_t block,
+                                                 void *q_row, void *q_col_pad, float *s_row_t,
+                                                 float *s_col_pad, int64_t *vk_lens,
+                                                 int64_t *vk_offs, int fmt, pta_stream_t stream);
+
+/* MXFP8 (block 32, E8M0): x[G, M, N].  Rowwise output q_row[G*M, N_pad],
+ * e_row[G*M, N_pad/32]; colwise output (transposed) q_col[G*N, M_pad],
+ * e_col[G*N, M_pad/32]; pads are 128 and padded elements are 0.  Either pair
+ * may be NULL.  use_2d_* shares one exponent per 32 x 32 tile.
+ * Replaces quantize_mxfp8 / quantize_mxfp8_dual (quantization.cpp:736-967). */
+int pta_quantize_mxfp8(const void *x, int in_dtype, int64_t G, int64_t M, int64_t N, void *q_row,
+                       uint8_t *e_row, int use_2d_row, void *q_col, uint8_t *e_col, int use_2d_col,
+                       int fmt, pta_stream_t stream);
+
+/* ============================================================================
+ * Dequantization: y = out_dtype(float(q) * scale_inv)
+ * ========================================================================== */
+
+/* Replaces dequantize_fp8_tensorwise (quantization.cpp:207+). */
+int pta_dequantize_fp8_tensorwise(const void *q, int fmt, int64_t n, const float *scale_inv,
+                                  void *y, int out_dtype, pta_stream_t stream);
+
+/* q viewed as [outer, len, inner], scale_inv[outer*inner].
+ * Replaces dequantize_fp8_rowwise (quantization.cpp). */
+int pta_dequantize_fp8_rowwise(const void *q, int fmt, int64_t outer, int64_t len, int64_t inner,
+                               const float *scale_inv, void *y, int out_dtype, pta_stream_t stream);
+
+/* mode 0: block x 1 (axis 0), mode 1: 1 x block (axis 1), mode 2: 2-D weight
+ * tiles over [B, M, N].  Replaces dequant_fp8_blockwise(_for_weight)_impl
+ * (quantization_impl.py:139-226). */
+int pta_dequantize_fp8_blockwise(const void *q, int fmt, int64_t B, int64_t M, int64_t N,
+                                 int64_t block, int mode, const float *scale_inv, void *y,
+                                 int out_dtype, pta_stream_t stream);
+
+/* MX dequant of q[R, C] with e8m0[R, C/32] along rows; transpose_out = 1 writes
+ * y as [C, R] (the colwise direction).  Replaces dequantize_mxfp8
+ * (csrc/kernels/quantization/dequantization_mxfp8.cu:26-111). */
+int pta_dequantize_mxfp8(const void *q, int fmt, int64_t R, int64_t C, const uint8_t *e8m0,
+                         int transpose_out, void *y, int out_dtype, pta_stream_t stream);
+
+/* ============================================================================
+ * Layout helpers
+ * ========================================================================== */
+
+/* Byte transpose x[B, M, N] -> y[B, N, M].  Replaces transpose_2d
+ * (csrc/pytorch/transpose/transpose.cpp) for fp8 tensors. */
+int pta_transpose_u8(const void *x, int64_t B, int64_t M, int64_t N, void *y, pta_stream_t stream);
+
+/* offs[0] = 0, offs[i+1] = offs[i] + lens[i] (int64, device).
+ * Replaces grouped_gemm_compute_offs (csrc/pytorch/grouped_gemm/ck_grouped_gemm.cpp:63-80). */
+int pta_grouped_compute_offs(const int64_t *lens, int64_t *offs, int64_t G, pta_stream_t stream);
+
+/* padded_offs[0] = 0, padded_offs[g+1] = padded_offs[g] + roundup(offs[g+1] - offs[g], align)
+ * (int64, device).  Replaces the padded-offset computation of
+ * csrc/kernels/quantization/quantization_blockwise.cu:16-51. */
+int pta_grouped_compute_padded_offs(const int64_t *offs, int64_t *padded_offs, int64_t G,
+                                    int64_t align, pta_stream_t stream);
+
+/* ============================================================================
+ * GEMM
+ * ========================================================================== */
+
+/* C = op(A) @ op(B) with fp32 accumulation and fp8 inputs, output in c_dtype
+ * (PTA_BF16 / PTA_F16 / PTA_F32).  Logical shapes: op(A) [M,K], op(B) [K,N];
+ * trans_c = 1 stores C^T ([N, M]).
+ * granularity: PTA_TENSORWISE (a_scale, b_scale device scalars),
+ *              PTA_ROWWISE   (a_scale[M], b_scale[N]),
+ *              PTA_BLOCKWISE (see below),
+ *              PTA_MX_BLOCKWISE (NT only: e8m0 a_scale[M, K/32], b_scale[N, K/32]).
+ * Blockwise scale layouts are those of the reference Triton wrapper
+ * (primus_turbo/triton/gemm/gemm_fp8_kernel.py:1013-1154):
+ *   NT: A[M,K] a_scale[M,K/128];  B[N,K] b_scale[N/128,K/128]
+ *   NN: A[M,K] a_scale[M,K/128];  B[K,N] b_scale[K/128,N/128]
+ *   TN: A[K,M] a_scale[K/128,M];  B[K,N] b_scale[K/128,N]
+ * workspace may be NULL when pta_gemm_fp8_workspace_size() returns 0 for
+ * these arguments.  Replaces gemm_fp8_impl
+ * (primus_turbo/pytorch/kernels/gemm/gemm_fp8_impl.py:438-467) and the native
+ * hipblaslt/ck/turbo_gemm_fp8 ops behind it. */
+size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b,
+                                   int granularity);
+int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int trans_a, const void *b,
+                 int b_fmt, const void *b_scale, int trans_b, void *c, int c_dtype, int trans_c,
+                 int64_t M, int64_t N, int64_t K, int granularity, void *workspace,
+                 size_t workspace_bytes, pta_stream_t stream);
+
+/* Kernel-level NT entry: C[m, n] = sum_k A[m, k] * B[n, k] with explicit row
+ * strides and explicit scale addressing.  Blockwise scales are read as
+ * a_scale[r * sa_m + kb * sa_k] with r = m (or m / 128 when a_scale_2d) and
+ * kb = k / 128; likewise for B.  MX scales are e8m0 bytes at
+ * a_scale[m * sa_m + k / 32].  *_scale_bytes bound the scale arrays.  This has
+ * no single counterpart in the reference; it is the kernel interface below
+ * gemm_fp8_impl that the autograd functions use to consume transposed
+ * quantized copies without extra layout passes. */
+int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt,
+                            int64_t ldb, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N,
+                            int64_t K, int granularity, const void *a_scale, int64_t sa_m,
+                            int64_t sa_k, int a_scale_2d, int64_t a_scale_bytes,
+                            const void *b_scale, int64_t sb_m, int64_t sb_k, int b_scale_2d,
+                            int64_t b_scale_bytes, pta_stream_t stream);
+
+/* Grouped GEMM over G groups of rows of A (M-grouped, forward / dgrad):
+ * out[offs[g]:offs[g+1]] = A[offs[g]:offs[g+1]] @ op(B[g]), B[G, N, K]
+ * (trans_b = 1) or [G, K, N].  group_offs[G+1] on device, never read by the host.
+ * Rows [group_offs[G], M_total) of out are set to 0.
+ * Blockwise: a_scale transposed [K/128, M_total], b_scale[G, N/128, K/128]
+ * (trans_b = 1) or [G, K/128, N/128].  Tensorwise: device scalars.
+ * Rowwise: a_scale[M_total], b_scale[G, N].
+ * Replaces grouped_gemm_fp8_impl
+ * (primus_turbo/pytorch/kernels/grouped_gemm/grouped_gemm_fp8_impl.py:817-859). */
+size_t pta_grouped_gemm_fp8_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G,
+                                           int trans_b, int granularity);
+int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scale, const void *b, int b_fmt,
+                         const void *b_scale, int trans_b, const int64_t *group_offs, int64_t G,
+                         int64_t M_total, int64_t N, int64_t K, void *out, int c_dtype,
+                         int granularity, int num_cu, void *workspace, size_t workspace_bytes,
+                         pta_stream_t stream);
+
+/* Variable-K grouped GEMM (wgrad): for each g,
+ * out[g] = op_c( lhs[seg_g]^T @ rhs[seg_g] ) with seg_g = rows
+ * [group_offs[g], group_offs[g+1]) of lhs[M_total, OUT_M] and rhs[M_total, OUT_N];
+ * out[G, OUT_M, OUT_N] (trans_c = 0) or [G, OUT_N, OUT_M] (trans_c = 1).
+ * Blockwise: segments are 128-aligned (group_offs multiples of 128),
+ * lhs_scale[M_total/128, OUT_M], rhs_scale[M_total/128, OUT_N].  Tensorwise:
+ * device scalars, any group sizes.  Empty groups produce zero output.  Replaces grouped_gemm_fp8_variable_k_impl
+ * (grouped_gemm_fp8_impl.py:862-901). */
+size_t pta_grouped_gemm_fp8_variable_k_workspace_size(int64_t M_total, int64_t OUT_M,
+                                                      int64_t OUT_N, int64_t G, int granularity);
+int pta_grouped_gemm_fp8_variable_k(const void *lhs, int lhs_fmt, const void *lhs_scale,
+                                    const void *rhs, int rhs_fmt, const void *rhs_scale,
+                                    const int64_t *group_offs, int64_t G, int64_t M_total,
+                                    int64_t OUT_M, int64_t OUT_N, void *out, int c_dtype,
+                                    int trans_c, int granularity, int num_cu, void *workspace,
+                                    size_t workspace_bytes, pta_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRIMUS_TURBO_AMD_H */

@@ -1,0 +1,125 @@
+// Driver for the reference's own HIP quantization kernels -- TEST INFRASTRUCTURE ONLY.
+//
+// oracle/Makefile.ref compiles this file together with the reference's kernel
+// sources, where they lie under /root/reference/csrc, into oracle/_ref/libref_quant.so.
+// The extern "C" functions below replay the host-side sequence of the
+// reference's native ops (csrc/pytorch/quantization/quantization.cpp:42-206,
+// 1382-1476) on caller-provided device buffers, so GPU parity tests can compare
+// the bytes and scales of this repository's kernels with the reference's.
+// Input is bf16; fmt 0 = e4m3fn, 1 = e5m2.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "primus_turbo/quantization.h"
+#include "primus_turbo/reduce.h"
+
+using namespace primus_turbo;
+using bf16 = dtype::bfloat16;
+
+namespace {
+float fp8_max(int fmt) { return fmt == 0 ? 448.0f : 57344.0f; }
+} // namespace
+
+extern "C" {
+
+// bytes of workspace needed by ref_quant_tensorwise (amax, scale, reduce scratch)
+int64_t ref_tensorwise_ws_bytes(int64_t n) {
+    return 256 + get_reduce_row_workspace_sizes<float>(1, n);
+}
+
+// quantization.cpp:42-88 (no precomputed scale)
+int ref_quant_tensorwise(const void *x, int64_t n, int fmt, void *q, float *scale_inv, void *ws,
+                         void *stream_) {
+    hipStream_t st     = reinterpret_cast<hipStream_t>(stream_);
+    float      *amax   = reinterpret_cast<float *>(ws);
+    float      *scale  = amax + 1;
+    void       *rws    = reinterpret_cast<char *>(ws) + 256;
+    const int64_t rsz  = get_reduce_row_workspace_sizes<float>(1, n);
+    reduce_row<bf16, float, float>(PrimusTurboReduceOp::REDUCE_ABS_MAX, reinterpret_cast<const bf16 *>(x),
+                                   amax, 1, n, rsz, rws, st);
+    compute_scale_from_amax<float>(amax, fp8_max(fmt), scale, scale_inv, 1, st);
+    if (fmt == 0)
+        quantize_tensorwise_impl<bf16, dtype::float8_e4m3>(reinterpret_cast<const bf16 *>(x), scale,
+                                                           reinterpret_cast<dtype::float8_e4m3 *>(q), n, st);
+    else
+        quantize_tensorwise_impl<bf16, dtype::float8_e5m2>(reinterpret_cast<const bf16 *>(x), scale,
+                                                           reinterpret_cast<dtype::float8_e5m2 *>(q), n, st);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// quantization.cpp:155-167 (row-major: axis is the last dim); scale buffer [outer]
+int ref_quant_rowwise_last(const void *x, int64_t outer, int64_t inner, int fmt, void *q, float *scale,
+                           float *scale_inv, void *stream_) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream_);
+    if (fmt == 0)
+        quantize_rowwise_row_major_impl<bf16, dtype::float8_e4m3, float, false>(
+            reinterpret_cast<const bf16 *>(x), scale, scale_inv, reinterpret_cast<dtype::float8_e4m3 *>(q),
+            outer, inner, st);
+    else
+        quantize_rowwise_row_major_impl<bf16, dtype::float8_e5m2, float, false>(
+            reinterpret_cast<const bf16 *>(x), scale, scale_inv, reinterpret_cast<dtype::float8_e5m2 *>(q),
+            outer, inner, st);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int64_t ref_rowwise_col_ws_bytes(int64_t B, int64_t M, int64_t N) {
+    return 256 + B * N * 4 + get_reduce_col_workspace_sizes<float>(B, M, N);
+}
+
+// quantization.cpp:168-201 (x viewed [B, M, N], reduced over M); scale buffers [B*N]
+int ref_quant_rowwise_col(const void *x, int64_t B, int64_t M, int64_t N, int fmt, void *q, float *scale,
+                          float *scale_inv, void *ws, void *stream_) {
+    hipStream_t   st   = reinterpret_cast<hipStream_t>(stream_);
+    float        *amax = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + 256);
+    void         *rws  = reinterpret_cast<char *>(ws) + 256 + B * N * 4;
+    const int64_t rsz  = get_reduce_col_workspace_sizes<float>(B, M, N);
+    reduce_col<bf16, float, float>(PrimusTurboReduceOp::REDUCE_ABS_MAX, reinterpret_cast<const bf16 *>(x), amax,
+                                   B, M, N, rsz, rws, st);
+    compute_scale_from_amax<float>(amax, fp8_max(fmt), scale, scale_inv, B * N, st);
+    if (fmt == 0)
+        quantize_rowwise_col_major_impl<bf16, dtype::float8_e4m3, float>(
+            reinterpret_cast<const bf16 *>(x), scale, scale_inv, reinterpret_cast<dtype::float8_e4m3 *>(q), B, M,
+            N, st);
+    else
+        quantize_rowwise_col_major_impl<bf16, dtype::float8_e5m2, float>(
+            reinterpret_cast<const bf16 *>(x), scale, scale_inv, reinterpret_cast<dtype::float8_e5m2 *>(q), B, M,
+            N, st);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// quantization.cpp:1442-1476
+int ref_quant_weight(const void *w, int64_t B, int64_t M, int64_t N, int fmt, void *q, float *s, void *stream_) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream_);
+    if (fmt == 0)
+        quantize_blockwise_for_weight_impl<bf16, dtype::float8_e4m3>(
+            reinterpret_cast<const bf16 *>(w), reinterpret_cast<dtype::float8_e4m3 *>(q), s, B, M, N, fp8_max(fmt),
+            st);
+    else
+        quantize_blockwise_for_weight_impl<bf16, dtype::float8_e5m2>(
+            reinterpret_cast<const bf16 *>(w), reinterpret_cast<dtype::float8_e5m2 *>(q), s, B, M, N, fp8_max(fmt),
+            st);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// quantization.cpp:1382-1439
+int ref_quant_segment(const void *x, int64_t M, int64_t N, int64_t G, const int64_t *group_lens,
+                      const int64_t *group_offs, int fmt, void *q_row, void *q_col, float *s_row, float *s_col,
+                      int64_t *vk_lens, int64_t *vk_offs, void *stream_) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream_);
+    compute_padded_group_offs<int64_t>(group_lens, vk_lens, vk_offs, G, 128, st);
+    const int64_t Mpad = M + G * 128;
+    if (fmt == 0)
+        quantize_blockwise_segment_m_row_col_impl<bf16, dtype::float8_e4m3>(
+            reinterpret_cast<const bf16 *>(x), reinterpret_cast<dtype::float8_e4m3 *>(q_row),
+            reinterpret_cast<dtype::float8_e4m3 *>(q_col), s_row, s_col, group_offs, vk_offs, M, N, Mpad,
+            static_cast<int>(G), fp8_max(fmt), st);
+    else
+        quantize_blockwise_segment_m_row_col_impl<bf16, dtype::float8_e5m2>(
+            reinterpret_cast<const bf16 *>(x), reinterpret_cast<dtype::float8_e5m2 *>(q_row),
+            reinterpret_cast<dtype::float8_e5m2 *>(q_col), s_row, s_col, group_offs, vk_offs, M, N, Mpad,
+            static_cast<int>(G), fp8_max(fmt), st);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+} // extern "C"

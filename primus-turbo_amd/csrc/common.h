@@ -1,0 +1,214 @@
+// Shared host/device helpers for the gfx950 FP8 linear-path library.
+//
+// Everything here is MI355X-specific: wave64, OCP fp8 conversion through
+// v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 (round-to-nearest-even), DPP lane
+// exchanges for reductions.  No CUDA shims, no multi-architecture paths.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "primus_turbo_amd.h"
+
+namespace pta {
+
+// ---------------------------------------------------------------------------
+// error reporting (thread-local message, int status codes at the C boundary)
+// ---------------------------------------------------------------------------
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define PTA_CHECK_ARG(cond, ...)                                                                   \
+    do {                                                                                           \
+        if (!(cond)) {                                                                             \
+            ::pta::set_error(__VA_ARGS__);                                                         \
+            return PTA_ERR_INVALID_ARG;                                                            \
+        }                                                                                          \
+    } while (0)
+
+#define PTA_CHECK_HIP(expr)                                                                        \
+    do {                                                                                           \
+        hipError_t _e = (expr);                                                                    \
+        if (_e != hipSuccess) {                                                                    \
+            ::pta::set_error("HIP error '%s' at %s:%d", hipGetErrorString(_e), __FILE__,          \
+                             __LINE__);                                                            \
+            return PTA_ERR_HIP;                                                                    \
+        }                                                                                          \
+    } while (0)
+
+#define PTA_CHECK_LAUNCH() PTA_CHECK_HIP(hipGetLastError())
+
+inline hipStream_t as_stream(pta_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline float fp8_max_host(int fmt) { return fmt == PTA_E5M2 ? 57344.0f : 448.0f; }
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+struct bf16_t {
+    uint16_t bits;
+};
+struct f16_t {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+    _Float16 h;
+    uint16_t s = static_cast<uint16_t>(b);
+    __builtin_memcpy(&h, &s, 2);
+    return static_cast<float>(h);
+}
+
+// Convert an fp32 value to bf16 bits with round-to-nearest-even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = static_cast<_Float16>(f);
+    uint16_t s;
+    __builtin_memcpy(&s, &h, 2);
+    return s;
+}
+
+// Load 8 consecutive input elements as fp32 (16-byte aligned source for 16-bit
+// types, two 16-byte loads for fp32).
+template <int IN_DT> struct InTraits;
+template <> struct InTraits<PTA_BF16> {
+    static constexpr int bytes = 2;
+};
+template <> struct InTraits<PTA_F16> {
+    static constexpr int bytes = 2;
+};
+template <> struct InTraits<PTA_F32> {
+    static constexpr int bytes = 4;
+};
+
+template <int IN_DT>
+__device__ __forceinline__ float load_scalar(const void *base, int64_t idx) {
+    if constexpr (IN_DT == PTA_F32) {
+        return reinterpret_cast<const float *>(base)[idx];
+    } else if constexpr (IN_DT == PTA_BF16) {
+        return bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(base)[idx]);
+    } else {
+        return f16_bits_to_f32(reinterpret_cast<const uint16_t *>(base)[idx]);
+    }
+}
+
+// 8 elements from a 16-byte-aligned address (two dwordx4 for fp32).
+template <int IN_DT>
+__device__ __forceinline__ void load8(const void *base, int64_t idx, float (&v)[8]) {
+    if constexpr (IN_DT == PTA_F32) {
+        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(base) + idx);
+        float4        a = p[0];
+        float4        b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(base) + idx);
+        uint4        w = p[0];
+        uint32_t     ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (IN_DT == PTA_BF16) {
+                v[2 * i]     = __uint_as_float(ws[i] << 16);
+                v[2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
+            } else {
+                v[2 * i]     = f16_bits_to_f32(ws[i] & 0xffffu);
+                v[2 * i + 1] = f16_bits_to_f32(ws[i] >> 16);
+            }
+        }
+    }
+}
+
+// Pack four fp32 values (already clamped to the format's range) into four OCP
+// fp8 bytes with round-to-nearest-even.  FMT: PTA_E4M3 or PTA_E5M2.
+template <int FMT> __device__ __forceinline__ uint32_t cvt4_fp8(float a, float b, float c, float d) {
+    int w;
+    if constexpr (FMT == PTA_E4M3) {
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    } else {
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+    }
+    return static_cast<uint32_t>(w);
+}
+
+template <int FMT> __device__ __forceinline__ uint8_t cvt1_fp8(float a) {
+    return static_cast<uint8_t>(cvt4_fp8<FMT>(a, 0.f, 0.f, 0.f) & 0xffu);
+}
+
+template <int FMT> __device__ __forceinline__ constexpr float fp8_max() {
+    return FMT == PTA_E4M3 ? 448.0f : 57344.0f;
+}
+
+// quant op of the reference: clamp(x * scale, -max, max); fmin/fmax send NaN to +max.
+template <int FMT> __device__ __forceinline__ float qclamp(float x, float scale) {
+    const float v = x * scale;
+    return fmaxf(fminf(v, fp8_max<FMT>()), -fp8_max<FMT>());
+}
+
+template <int FMT>
+__device__ __forceinline__ uint32_t quant4(const float *v, float scale) {
+    return cvt4_fp8<FMT>(qclamp<FMT>(v[0], scale), qclamp<FMT>(v[1], scale),
+                         qclamp<FMT>(v[2], scale), qclamp<FMT>(v[3], scale));
+}
+
+// ---- DPP lane exchange (wave64, rows of 16 lanes) ---------------------------
+// ctrl values from the GCN/CDNA DPP encoding.
+#define PTA_DPP_QUAD_XOR1 0xB1
+#define PTA_DPP_QUAD_XOR2 0x4E
+#define PTA_DPP_ROW_HALF_MIRROR 0x141
+#define PTA_DPP_ROW_MIRROR 0x140
+
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// max over groups of 8 consecutive lanes (result in every lane of the group)
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<PTA_DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp_f<PTA_DPP_QUAD_XOR2>(v));
+    v = fmaxf(v, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(v));
+    return v;
+}
+
+// max over groups of 16 consecutive lanes
+__device__ __forceinline__ float max16(float v) {
+    v = max8(v);
+    v = fmaxf(v, dpp_f<PTA_DPP_ROW_MIRROR>(v));
+    return v;
+}
+
+// max over the whole wave (result valid in every lane)
+__device__ __forceinline__ float max64(float v) {
+    v = max16(v);
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+// scale = max / fmaxf(amax, eps) and its inverse 1/scale, both IEEE divisions
+// (hipcc emits correctly rounded fp32 division unless fast-math is requested,
+// and this library is never built with fast-math).
+template <int FMT> __device__ __forceinline__ float scale_from_amax(float amax, float eps) {
+    return fp8_max<FMT>() / fmaxf(amax, eps);
+}
+
+// Wave-uniform helpers
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & 63; }
+
+} // namespace pta

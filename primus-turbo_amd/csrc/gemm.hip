@@ -1,0 +1,153 @@
+// Host side of the dense FP8 GEMM: layout reduction to NT and scale-stride
+// bookkeeping (the kernel itself lives in gemm_kernel.h).
+#include "gemm_kernel.h"
+
+namespace pta {
+using namespace gemm_detail;
+
+// Entry used by the dense and grouped front ends: NT problem fully described.
+int gemm_nt_launch(const uint8_t *a, int fa, int64_t lda, const uint8_t *b, int fb, int64_t ldb,
+                   void *c, int out_dt, int64_t ldc, int64_t M, int64_t N, int64_t K, int sm,
+                   bool a2d, bool b2d, const void *sa, int64_t sa_m, int64_t sa_k, int64_t sa_bytes,
+                   const void *sb, int64_t sb_m, int64_t sb_k, int64_t sb_bytes, hipStream_t st) {
+    GemmArgs g{};
+    g.a = a; g.b = b; g.c = c; g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
+    g.sa = sa; g.sb = sb; g.sa_m = sa_m; g.sa_k = sa_k; g.sb_m = sb_m; g.sb_k = sb_k;
+    g.sa_bytes = sa_bytes; g.sb_bytes = sb_bytes;
+    g.tiles_m = static_cast<int>(cdiv(M, BM));
+    g.tiles_n = static_cast<int>(cdiv(N, BN));
+    g.group_m = 4;
+    g.aligned_c = ((ldc * (out_dt == PTA_F32 ? 4 : 2)) % 16 == 0) && aligned16(c);
+    if (sm == SM_TENSOR) return dispatch_tensor(g, fa, fb, out_dt, st);
+    if (sm == SM_ROW) return dispatch_row(g, fa, fb, out_dt, st);
+    if (sm == SM_MX) return dispatch_mx(g, fa, fb, out_dt, st);
+    if (a2d && b2d) {
+        set_error("blockwise GEMM with 2-D scales on both operands is not supported");
+        return PTA_ERR_UNSUPPORTED;
+    }
+    return dispatch_block(g, a2d, b2d, fa, fb, out_dt, st);
+}
+
+} // namespace pta
+
+using namespace pta;
+
+namespace {
+int gran_to_sm(int gran) {
+    switch (gran) {
+    case PTA_TENSORWISE: return SM_TENSOR;
+    case PTA_ROWWISE: return SM_ROW;
+    case PTA_BLOCKWISE: return SM_BLOCK;
+    case PTA_MX_BLOCKWISE: return SM_MX;
+    default: return -1;
+    }
+}
+} // namespace
+
+extern "C" size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, int trans_a,
+                                              int trans_b, int /*granularity*/) {
+    size_t ws = 0;
+    if (trans_a) ws += static_cast<size_t>(cdiv(M * K, 256) * 256);
+    if (!trans_b) ws += static_cast<size_t>(cdiv(N * K, 256) * 256);
+    return ws;
+}
+
+extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int trans_a, const void *b,
+                            int b_fmt, const void *b_scale, int trans_b, void *c, int c_dtype,
+                            int trans_c, int64_t M, int64_t N, int64_t K, int granularity,
+                            void *workspace, size_t workspace_bytes, pta_stream_t stream) {
+    clear_error();
+    const int sm = gran_to_sm(granularity);
+    PTA_CHECK_ARG(sm >= 0, "unknown granularity %d", granularity);
+    PTA_CHECK_ARG(a && b && c && a_scale && b_scale, "NULL pointer argument");
+    PTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "negative shape");
+    PTA_CHECK_ARG((a_fmt == PTA_E4M3 || a_fmt == PTA_E5M2) && (b_fmt == PTA_E4M3 || b_fmt == PTA_E5M2),
+                  "unsupported fp8 format");
+    PTA_CHECK_ARG(c_dtype == PTA_BF16 || c_dtype == PTA_F16 || c_dtype == PTA_F32, "unsupported output dtype");
+    PTA_CHECK_ARG(K % 16 == 0, "K must be a multiple of 16 (got %lld)", (long long)K);
+    PTA_CHECK_ARG(!(trans_a && trans_b), "the TT layout is not supported");
+    if (sm == SM_MX) {
+        PTA_CHECK_ARG(!trans_a && trans_b, "MX_BLOCKWISE supports the NT layout only");
+        PTA_CHECK_ARG(K % 128 == 0, "MX_BLOCKWISE needs K %% 128 == 0");
+    }
+    if (M == 0 || N == 0) return PTA_OK;
+    PTA_CHECK_ARG(aligned16(a) && aligned16(b), "A and B must be 16-byte aligned");
+    hipStream_t st = as_stream(stream);
+    if (K == 0) {
+        const size_t eb = c_dtype == PTA_F32 ? 4 : 2;
+        PTA_CHECK_HIP(hipMemsetAsync(c, 0, static_cast<size_t>(M * N) * eb, st));
+        return PTA_OK;
+    }
+    const size_t need = pta_gemm_fp8_workspace_size(M, N, K, trans_a, trans_b, granularity);
+    PTA_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                  "workspace of %zu bytes required", need);
+
+    // ---- reduce to NT: A' [M, K] K-contiguous, B' [N, K] K-contiguous ------
+    const uint8_t *ap = static_cast<const uint8_t *>(a);
+    const uint8_t *bp = static_cast<const uint8_t *>(b);
+    uint8_t       *wsp = static_cast<uint8_t *>(workspace);
+    if (trans_a) { // A stored [K, M]
+        if (int rc = pta_transpose_u8(a, 1, K, M, wsp, stream)) return rc;
+        ap = wsp;
+        wsp += cdiv(M * K, 256) * 256;
+    }
+    if (!trans_b) { // B stored [K, N]
+        if (int rc = pta_transpose_u8(b, 1, K, N, wsp, stream)) return rc;
+        bp = wsp;
+    }
+    // scale strides in the NT view
+    bool    a2d = false, b2d = false;
+    int64_t sa_m = 0, sa_k = 0, sb_m = 0, sb_k = 0;
+    const int64_t kb = cdiv(K, 128);
+    if (sm == SM_BLOCK) {
+        if (!trans_a) { sa_m = kb; sa_k = 1; }     // [M, K/128]
+        else { sa_m = 1; sa_k = M; }               // [K/128, M]
+        if (trans_b) { b2d = true; sb_m = kb; sb_k = 1; }                 // [N/128, K/128]
+        else if (!trans_a) { b2d = true; sb_m = 1; sb_k = cdiv(N, 128); } // NN: [K/128, N/128]
+        else { b2d = false; sb_m = 1; sb_k = N; }                         // TN: [K/128, N]
+    } else if (sm == SM_MX) {
+        sa_m = K / 32; sb_m = K / 32;
+    }
+    // extent of each scale array in bytes
+    int64_t sa_bytes = 4, sb_bytes = 4;
+    if (sm == SM_ROW) { sa_bytes = M * 4; sb_bytes = N * 4; }
+    if (sm == SM_BLOCK) {
+        sa_bytes = M * kb * 4;
+        sb_bytes = (b2d ? cdiv(N, 128) : N) * kb * 4;
+    }
+    if (sm == SM_MX) { sa_bytes = M * (K / 32); sb_bytes = N * (K / 32); }
+    if (!trans_c) {
+        return gemm_nt_launch(ap, a_fmt, K, bp, b_fmt, K, c, c_dtype, N, M, N, K, sm, a2d, b2d,
+                              a_scale, sa_m, sa_k, sa_bytes, b_scale, sb_m, sb_k, sb_bytes, st);
+    }
+    // C^T[n, m] = sum_k B'[n,k] A'[m,k]: swap the operands
+    return gemm_nt_launch(bp, b_fmt, K, ap, a_fmt, K, c, c_dtype, M, N, M, K, sm, b2d, a2d,
+                          b_scale, sb_m, sb_k, sb_bytes, a_scale, sa_m, sa_k, sa_bytes, st);
+}
+
+extern "C" int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt,
+                                       int64_t ldb, void *c, int c_dtype, int64_t ldc, int64_t M,
+                                       int64_t N, int64_t K, int granularity, const void *a_scale,
+                                       int64_t sa_m, int64_t sa_k, int a_scale_2d,
+                                       int64_t a_scale_bytes, const void *b_scale, int64_t sb_m,
+                                       int64_t sb_k, int b_scale_2d, int64_t b_scale_bytes,
+                                       pta_stream_t stream) {
+    clear_error();
+    const int sm = gran_to_sm(granularity);
+    PTA_CHECK_ARG(sm >= 0, "unknown granularity %d", granularity);
+    PTA_CHECK_ARG(a && b && c && a_scale && b_scale, "NULL pointer argument");
+    PTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && lda >= K && ldb >= K && ldc >= N, "bad shape / strides");
+    PTA_CHECK_ARG((a_fmt == PTA_E4M3 || a_fmt == PTA_E5M2) && (b_fmt == PTA_E4M3 || b_fmt == PTA_E5M2),
+                  "unsupported fp8 format");
+    PTA_CHECK_ARG(c_dtype == PTA_BF16 || c_dtype == PTA_F16 || c_dtype == PTA_F32, "unsupported output dtype");
+    PTA_CHECK_ARG(K % 16 == 0 && lda % 16 == 0 && ldb % 16 == 0, "K and row strides must be multiples of 16");
+    PTA_CHECK_ARG(aligned16(a) && aligned16(b), "A and B must be 16-byte aligned");
+    PTA_CHECK_ARG(!(a_scale_2d && b_scale_2d), "2-D scales on both operands are not supported");
+    if (M == 0 || N == 0 || K == 0) {
+        PTA_CHECK_ARG(K != 0 || M == 0 || N == 0, "K == 0 is not supported by the strided entry");
+        return PTA_OK;
+    }
+    return gemm_nt_launch(static_cast<const uint8_t *>(a), a_fmt, lda, static_cast<const uint8_t *>(b), b_fmt,
+                          ldb, c, c_dtype, ldc, M, N, K, sm, a_scale_2d != 0, b_scale_2d != 0, a_scale, sa_m,
+                          sa_k, a_scale_bytes, b_scale, sb_m, sb_k, b_scale_bytes, as_stream(stream));
+}

@@ -1,0 +1,508 @@
+// Blockwise FP8 quantization on gfx950: 1 x 128 (row), 128 x 1 (col), dual,
+// 128 x 128 weight tiles and the grouped "segment" variant.
+//
+// One workgroup (4 waves, 256 lanes) owns a 128 x 128 input tile.  Lane t owns
+// 4 consecutive rows (4*(t>>3) .. +3) of a 16-column segment (16*(t&7) .. +15):
+//   * bf16 input is read once with 16-byte loads (a wave covers 8 rows x 256 B);
+//   * row amax = max over the lane's 16 values, then over the 8 consecutive lanes
+//     of the row (3 DPP steps, no LDS);
+//   * col amax = max over the lane's 4 rows, then rotate-by-8 DPP inside each
+//     16-lane row, then a 16 x 128 LDS table reduced by 128 lanes;
+//   * all 64 values stay in VGPRs between the reductions and the casts.
+// Scale arithmetic follows the reference exactly (eps 1e-4, IEEE divides):
+//   primus_turbo/triton/quantization/quant_blockwise.py:11-18 (1-D / dual)
+//   csrc/kernels/quantization/quantization_blockwise.cu:298-308 (weight)
+//   csrc/kernels/quantization/quantization_blockwise.cu:58-213 (segment)
+#include "common.h"
+
+namespace pta {
+
+namespace {
+
+constexpr int TILE = 128;
+constexpr int NT   = 256;
+
+enum : int {
+    QB_ROW     = 1,  // 1 x 128 scales, q_row [M, N]
+    QB_COL     = 2,  // 128 x 1 scales, q_col [M, N] or transposed
+    QB_COL_T   = 4,  // q_col written as [N, M]
+    QB_W2D     = 8,  // one scale per 128 x 128 tile (weight)
+    QB_W2D_T   = 16, // weight bytes also written transposed [N, M]
+    QB_SEGMENT = 32, // grouped rows: tile index is in 128-padded segment space
+};
+
+struct QBArgs {
+    const void *x;
+    int64_t     M, N;      // input rows / cols (per batch for W2D)
+    int64_t     batch_stride_x;
+    uint8_t    *q_row;     // ROW / W2D output
+    float      *s_row;     // ROW: [M, nb] (non-segment) or [nb, M] (segment)
+    uint8_t    *q_col;     // COL output
+    float      *s_col;     // COL: [mb, N]
+    uint8_t    *q_t;       // W2D_T output
+    float      *s_w;       // W2D: [B, mb, nb]
+    // segment mode
+    const int64_t *group_offs;  // [G+1]
+    const int64_t *padded_offs; // [G+1]
+    int64_t        G;
+};
+
+template <int IN_DT, int FMT, int MODE, bool VEC>
+__global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
+    const int     t     = threadIdx.x;
+    const int     lane  = t & 63;
+    const int     wave  = t >> 6;
+    const int     cseg  = t & 7;
+    const int     rgrp  = t >> 3;
+    const int64_t tm    = blockIdx.x; // tile row (padded space for SEGMENT)
+    const int64_t tn    = blockIdx.y;
+    const int64_t batch = blockIdx.z;
+    const int64_t M = args.M, N = args.N;
+    const int64_t n0 = tn * TILE + cseg * 16;
+
+    // ---- map tile rows to input rows -------------------------------------
+    int64_t row_base;      // input row of local row 0
+    int64_t row_lo, row_hi; // valid input rows [row_lo, row_hi)
+    int64_t pad_row0 = tm * TILE;
+    if constexpr ((MODE & QB_SEGMENT) != 0) {
+        const int64_t M_padded = args.padded_offs[args.G];
+        if (pad_row0 >= M_padded) return;
+        // binary search over the non-decreasing padded offsets
+        int64_t lo = 0, hi = args.G - 1;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if (args.padded_offs[mid] <= pad_row0) lo = mid;
+            else hi = mid - 1;
+        }
+        // the last g with padded_offs[g] <= pad_row0 owns a non-empty segment
+        const int64_t g = lo;
+        const int64_t orig_start = args.group_offs[g];
+        const int64_t orig_end   = args.group_offs[g + 1];
+        const int64_t pad_start  = args.padded_offs[g];
+        row_base = orig_start + (pad_row0 - pad_start);
+        row_lo   = orig_start;
+        row_hi   = orig_end < M ? orig_end : M;
+    } else {
+        row_base = pad_row0;
+        row_lo   = 0;
+        row_hi   = M;
+    }
+
+    const char *xb = reinterpret_cast<const char *>(args.x) +
+                     batch * args.batch_stride_x * InTraits<IN_DT>::bytes;
+
+    float v[4][16];
+    bool  rvalid[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t r = row_base + rgrp * 4 + i;
+        rvalid[i]       = (r >= row_lo) && (r < row_hi);
+        if (VEC && rvalid[i] && n0 + 16 <= N) {
+            float a[8], b[8];
+            load8<IN_DT>(xb, r * N + n0, a);
+            load8<IN_DT>(xb, r * N + n0 + 8, b);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                v[i][j]     = a[j];
+                v[i][j + 8] = b[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                v[i][j] = (rvalid[i] && n0 + j < N) ? load_scalar<IN_DT>(xb, r * N + n0 + j) : 0.0f;
+        }
+    }
+
+    __shared__ float s_part[16][TILE]; // col partial maxima (16 lane-rows x 128 cols)
+    __shared__ float s_cscale[TILE];
+    __shared__ float s_wmax[4];
+    __shared__ uint32_t s_tr[TILE][TILE / 4 + 1]; // transposed bytes, padded
+
+    // ---- row direction ----------------------------------------------------
+    if constexpr ((MODE & QB_ROW) != 0) {
+        const int64_t nb = (N + TILE - 1) / TILE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[i][j]));
+            a                = max8(a);
+            const float sc   = scale_from_amax<FMT>(a, 1e-4f);
+            const float sinv = 1.0f / sc;
+            const int64_t r  = row_base + rgrp * 4 + i;
+            if (rvalid[i]) {
+                uint32_t w[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) w[k] = quant4<FMT>(&v[i][4 * k], sc);
+                uint8_t *dst = args.q_row + r * N + n0;
+                if (VEC && n0 + 16 <= N) {
+                    *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        if (n0 + j < N) dst[j] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
+                }
+                if (cseg == 0) {
+                    if constexpr ((MODE & QB_SEGMENT) != 0) args.s_row[tn * M + r] = sinv;
+                    else args.s_row[r * nb + tn] = sinv;
+                }
+            }
+        }
+    }
+
+    // ---- column direction -------------------------------------------------
+    if constexpr ((MODE & QB_COL) != 0) {
+        float ca[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float a = fmaxf(fmaxf(fabsf(v[0][j]), fabsf(v[1][j])), fmaxf(fabsf(v[2][j]), fabsf(v[3][j])));
+            // lanes l and l^8 share a column segment inside each 16-lane row
+            a     = fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x128, 0xf, 0xf, false)));
+            ca[j] = a;
+        }
+        if ((lane & 15) < 8) {
+            const int prow = wave * 4 + (lane >> 4);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s_part[prow][cseg * 16 + j] = ca[j];
+        }
+        __syncthreads();
+        if (t < TILE) {
+            float a = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 16; ++p) a = fmaxf(a, s_part[p][t]);
+            const float sc = scale_from_amax<FMT>(a, 1e-4f);
+            s_cscale[t]    = sc;
+            const int64_t n = tn * TILE + t;
+            if (n < N) args.s_col[tm * N + n] = 1.0f / sc;
+        }
+        __syncthreads();
+        float cs[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) cs[j] = s_cscale[cseg * 16 + j];
+
+        if constexpr ((MODE & QB_COL_T) == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t prow = pad_row0 + rgrp * 4 + i; // output row (padded space)
+                bool          ok;
+                if constexpr ((MODE & QB_SEGMENT) != 0) ok = prow < args.padded_offs[args.G];
+                else ok = rvalid[i];
+                if (!ok) continue;
+                uint32_t w[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    w[k] = cvt4_fp8<FMT>(qclamp<FMT>(v[i][4 * k], cs[4 * k]), qclamp<FMT>(v[i][4 * k + 1], cs[4 * k + 1]),
+                                         qclamp<FMT>(v[i][4 * k + 2], cs[4 * k + 2]), qclamp<FMT>(v[i][4 * k + 3], cs[4 * k + 3]));
+                uint8_t *dst = args.q_col + prow * N + n0;
+                if (VEC && n0 + 16 <= N) {
+                    *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        if (n0 + j < N) dst[j] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
+                }
+            }
+        } else {
+            // transposed output q_col[N, M]: stage bytes column-major in LDS
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                uint32_t packed = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(v[i][j], cs[j]))) << (8 * i);
+                s_tr[cseg * 16 + j][rgrp] = packed;
+            }
+            __syncthreads();
+            // 128 output rows (n) x 128 bytes (m): 16-byte chunks; the row stride is
+            // M rounded up to 128 and the padding bytes (rows past M) are zero
+            const int64_t ldt = (M + TILE - 1) / TILE * TILE;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int     c   = it * NT + t;
+                const int     nl  = c >> 3;
+                const int     mc  = (c & 7) * 16;
+                const int64_t n   = tn * TILE + nl;
+                const int64_t m   = tm * TILE + mc;
+                if (n >= N) continue;
+                const uint32_t *src = &s_tr[nl][mc >> 2];
+                *reinterpret_cast<uint4 *>(args.q_col + n * ldt + m) = make_uint4(src[0], src[1], src[2], src[3]);
+            }
+        }
+    }
+
+    // ---- 128 x 128 weight tile --------------------------------------------
+    if constexpr ((MODE & QB_W2D) != 0) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[i][j]));
+        a = max64(a);
+        if (lane == 0) s_wmax[wave] = a;
+        __syncthreads();
+        a = fmaxf(fmaxf(s_wmax[0], s_wmax[1]), fmaxf(s_wmax[2], s_wmax[3]));
+        const float   sc  = scale_from_amax<FMT>(a, 1e-4f);
+        const int64_t mb  = (M + TILE - 1) / TILE, nb = (N + TILE - 1) / TILE;
+        if (t == 0) args.s_w[(batch * mb + tm) * nb + tn] = 1.0f / sc;
+        uint8_t *qb = args.q_row + batch * M * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t r = row_base + rgrp * 4 + i;
+            uint32_t      w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[k] = quant4<FMT>(&v[i][4 * k], sc);
+            if (!rvalid[i]) continue;
+            uint8_t *dst = qb + r * N + n0;
+            if (VEC && n0 + 16 <= N) {
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (n0 + j < N) dst[j] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
+            }
+        }
+        if constexpr ((MODE & QB_W2D_T) != 0) {
+            // transposed copy [B, N, M] through LDS
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                uint32_t packed = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(v[i][j], sc))) << (8 * i);
+                s_tr[cseg * 16 + j][rgrp] = packed;
+            }
+            __syncthreads();
+            const int64_t ldt = (M + TILE - 1) / TILE * TILE; // padded rows are zero
+            uint8_t      *qt  = args.q_t + batch * N * ldt;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int     c  = it * NT + t;
+                const int     nl = c >> 3;
+                const int     mc = (c & 7) * 16;
+                const int64_t n  = tn * TILE + nl;
+                const int64_t m  = tm * TILE + mc;
+                if (n >= N) continue;
+                const uint32_t *src = &s_tr[nl][mc >> 2];
+                *reinterpret_cast<uint4 *>(qt + n * ldt + m) = make_uint4(src[0], src[1], src[2], src[3]);
+            }
+        }
+    }
+}
+
+// vk_lens[g] = roundup(lens[g], 128); vk_offs = exclusive prefix sum (single workgroup)
+__global__ __launch_bounds__(256) void padded_offs_kernel(const int64_t *lens, int64_t *vk_lens,
+                                                          int64_t *vk_offs, int64_t G, int64_t align) {
+    __shared__ int64_t s_carry;
+    if (threadIdx.x == 0) {
+        s_carry    = 0;
+        vk_offs[0] = 0;
+    }
+    __syncthreads();
+    for (int64_t base = 0; base < G; base += 256) {
+        const int64_t g   = base + threadIdx.x;
+        const int64_t len = g < G ? lens[g] : 0;
+        const int64_t p   = (len + align - 1) / align * align;
+        // inclusive scan within the block (Hillis-Steele over LDS)
+        __shared__ int64_t s_scan[256];
+        s_scan[threadIdx.x] = p;
+        __syncthreads();
+        for (int off = 1; off < 256; off <<= 1) {
+            const int64_t add = threadIdx.x >= off ? s_scan[threadIdx.x - off] : 0;
+            __syncthreads();
+            s_scan[threadIdx.x] += add;
+            __syncthreads();
+        }
+        const int64_t carry = s_carry;
+        if (g < G) {
+            if (vk_lens) vk_lens[g] = p;
+            vk_offs[g + 1] = carry + s_scan[threadIdx.x];
+        }
+        __syncthreads();
+        if (threadIdx.x == 255) s_carry = carry + s_scan[255];
+        __syncthreads();
+    }
+}
+
+// padded_offs[g] = sum_{q<g} roundup(offs[q+1] - offs[q], align)
+__global__ __launch_bounds__(256) void offs_to_padded_offs_kernel(const int64_t *offs, int64_t *poffs,
+                                                                  int64_t G, int64_t align) {
+    __shared__ int64_t s_scan[256];
+    __shared__ int64_t s_carry;
+    if (threadIdx.x == 0) {
+        s_carry  = 0;
+        poffs[0] = 0;
+    }
+    __syncthreads();
+    for (int64_t base = 0; base < G; base += 256) {
+        const int64_t g   = base + threadIdx.x;
+        const int64_t len = g < G ? offs[g + 1] - offs[g] : 0;
+        s_scan[threadIdx.x] = (len + align - 1) / align * align;
+        __syncthreads();
+        for (int off = 1; off < 256; off <<= 1) {
+            const int64_t add = threadIdx.x >= off ? s_scan[threadIdx.x - off] : 0;
+            __syncthreads();
+            s_scan[threadIdx.x] += add;
+            __syncthreads();
+        }
+        const int64_t carry = s_carry;
+        if (g < G) poffs[g + 1] = carry + s_scan[threadIdx.x];
+        __syncthreads();
+        if (threadIdx.x == 255) s_carry = carry + s_scan[255];
+        __syncthreads();
+    }
+}
+
+template <int MODE>
+int launch_tile(const QBArgs &a, int in_dtype, int fmt, dim3 grid, bool vec, hipStream_t st) {
+#define PTA_QB_LAUNCH(IDT, F, V)                                                                   \
+    quant_block_tile_kernel<IDT, F, MODE, V><<<grid, NT, 0, st>>>(a)
+#define PTA_QB_FMT(IDT, V)                                                                         \
+    if (fmt == PTA_E4M3) PTA_QB_LAUNCH(IDT, PTA_E4M3, V);                                          \
+    else PTA_QB_LAUNCH(IDT, PTA_E5M2, V)
+#define PTA_QB_VEC(IDT)                                                                            \
+    if (vec) { PTA_QB_FMT(IDT, true); }                                                            \
+    else { PTA_QB_FMT(IDT, false); }
+    if (in_dtype == PTA_BF16) { PTA_QB_VEC(PTA_BF16) }
+    else if (in_dtype == PTA_F16) { PTA_QB_VEC(PTA_F16) }
+    else { PTA_QB_VEC(PTA_F32) }
+#undef PTA_QB_VEC
+#undef PTA_QB_FMT
+#undef PTA_QB_LAUNCH
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+bool vec_ok(const void *x, int in_dtype, int64_t N, std::initializer_list<const void *> outs) {
+    const int64_t eb = in_dtype == PTA_F32 ? 4 : 2;
+    if (!aligned16(x) || (N * eb) % 16 != 0 || N % 16 != 0) return false;
+    for (const void *p : outs)
+        if (p && !aligned16(p)) return false;
+    return true;
+}
+
+int check_common(const void *x, int in_dtype, int fmt, int64_t block) {
+    PTA_CHECK_ARG(x != nullptr, "input pointer is NULL");
+    PTA_CHECK_ARG(in_dtype == PTA_BF16 || in_dtype == PTA_F16 || in_dtype == PTA_F32,
+                  "unsupported input dtype code %d", in_dtype);
+    PTA_CHECK_ARG(fmt == PTA_E4M3 || fmt == PTA_E5M2, "unsupported fp8 format code %d", fmt);
+    PTA_CHECK_ARG(block == TILE, "block size %lld unsupported: only 128 is implemented",
+                  (long long)block);
+    return PTA_OK;
+}
+
+} // namespace
+} // namespace pta
+
+using namespace pta;
+
+extern "C" int pta_quantize_fp8_blockwise(const void *x, int in_dtype, int64_t M, int64_t N,
+                                          int64_t block, int axis, void *q, float *s, int fmt,
+                                          pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_common(x, in_dtype, fmt, block)) return rc;
+    PTA_CHECK_ARG(M >= 0 && N >= 0, "negative shape");
+    PTA_CHECK_ARG(axis == 0 || axis == 1, "axis must be 0 or 1");
+    if (M == 0 || N == 0) return PTA_OK;
+    QBArgs a{};
+    a.x = x; a.M = M; a.N = N;
+    dim3 grid(static_cast<uint32_t>(cdiv(M, TILE)), static_cast<uint32_t>(cdiv(N, TILE)), 1);
+    const bool v = vec_ok(x, in_dtype, N, {q});
+    if (axis == 1) {
+        a.q_row = static_cast<uint8_t *>(q); a.s_row = s;
+        return launch_tile<QB_ROW>(a, in_dtype, fmt, grid, v, as_stream(stream));
+    }
+    a.q_col = static_cast<uint8_t *>(q); a.s_col = s;
+    return launch_tile<QB_COL>(a, in_dtype, fmt, grid, v, as_stream(stream));
+}
+
+extern "C" int pta_quantize_fp8_blockwise_dual(const void *x, int in_dtype, int64_t M, int64_t N,
+                                               int64_t block, void *q_row, float *s_row,
+                                               void *q_col, float *s_col, int col_transposed,
+                                               int fmt, pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_common(x, in_dtype, fmt, block)) return rc;
+    PTA_CHECK_ARG(M >= 0 && N >= 0, "negative shape");
+    PTA_CHECK_ARG((q_row == nullptr) == (s_row == nullptr), "q_row/s_row must both be set or NULL");
+    PTA_CHECK_ARG((q_col == nullptr) == (s_col == nullptr), "q_col/s_col must both be set or NULL");
+    PTA_CHECK_ARG(q_row || q_col, "no output requested");
+    if (M == 0 || N == 0) return PTA_OK;
+    QBArgs a{};
+    a.x = x; a.M = M; a.N = N;
+    a.q_row = static_cast<uint8_t *>(q_row); a.s_row = s_row;
+    a.q_col = static_cast<uint8_t *>(q_col); a.s_col = s_col;
+    dim3       grid(static_cast<uint32_t>(cdiv(M, TILE)), static_cast<uint32_t>(cdiv(N, TILE)), 1);
+    PTA_CHECK_ARG(!col_transposed || aligned16(q_col), "transposed q_col must be 16-byte aligned");
+    const bool v = vec_ok(x, in_dtype, N, {q_row, col_transposed ? nullptr : q_col});
+    hipStream_t st = as_stream(stream);
+    if (q_row && q_col) {
+        return col_transposed ? launch_tile<QB_ROW | QB_COL | QB_COL_T>(a, in_dtype, fmt, grid, v, st)
+                              : launch_tile<QB_ROW | QB_COL>(a, in_dtype, fmt, grid, v, st);
+    }
+    if (q_row) return launch_tile<QB_ROW>(a, in_dtype, fmt, grid, v, st);
+    return col_transposed ? launch_tile<QB_COL | QB_COL_T>(a, in_dtype, fmt, grid, v, st)
+                          : launch_tile<QB_COL>(a, in_dtype, fmt, grid, v, st);
+}
+
+extern "C" int pta_quantize_fp8_blockwise_for_weight(const void *w, int in_dtype, int64_t B,
+                                                     int64_t M, int64_t N, int64_t block, void *q,
+                                                     float *s, void *q_t, int fmt,
+                                                     pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_common(w, in_dtype, fmt, block)) return rc;
+    PTA_CHECK_ARG(B >= 0 && M >= 0 && N >= 0, "negative shape");
+    PTA_CHECK_ARG(q != nullptr && s != nullptr, "q and s must be set");
+    if (B == 0 || M == 0 || N == 0) return PTA_OK;
+    PTA_CHECK_ARG(B <= 65535, "batch too large");
+    QBArgs a{};
+    a.x = w; a.M = M; a.N = N; a.batch_stride_x = M * N;
+    a.q_row = static_cast<uint8_t *>(q); a.s_w = s; a.q_t = static_cast<uint8_t *>(q_t);
+    dim3 grid(static_cast<uint32_t>(cdiv(M, TILE)), static_cast<uint32_t>(cdiv(N, TILE)),
+              static_cast<uint32_t>(B));
+    PTA_CHECK_ARG(!q_t || aligned16(q_t), "q_t must be 16-byte aligned");
+    const bool v = vec_ok(w, in_dtype, N, {q}) && (M * N * (in_dtype == PTA_F32 ? 4 : 2)) % 16 == 0;
+    hipStream_t st = as_stream(stream);
+    if (q_t) return launch_tile<QB_W2D | QB_W2D_T>(a, in_dtype, fmt, grid, v, st);
+    return launch_tile<QB_W2D>(a, in_dtype, fmt, grid, v, st);
+}
+
+extern "C" int pta_quantize_fp8_blockwise_segment_m_row_col(
+    const void *x, int in_dtype, int64_t M, int64_t N, int64_t G, const int64_t *group_lens,
+    const int64_t *group_offs, int64_t block, void *q_row, void *q_col_pad, float *s_row_t,
+    float *s_col_pad, int64_t *vk_lens, int64_t *vk_offs, int fmt, pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_common(x, in_dtype, fmt, block)) return rc;
+    PTA_CHECK_ARG(M >= 0 && N >= 0 && G >= 1, "bad shape");
+    PTA_CHECK_ARG(group_lens && group_offs && vk_offs && vk_lens, "group arrays must be set");
+    PTA_CHECK_ARG(q_row && q_col_pad && s_row_t && s_col_pad, "outputs must be set");
+    hipStream_t st = as_stream(stream);
+    padded_offs_kernel<<<1, 256, 0, st>>>(group_lens, vk_lens, vk_offs, G, TILE);
+    PTA_CHECK_LAUNCH();
+    if (N == 0) return PTA_OK;
+    const int64_t M_pad_max = M + G * TILE;
+    QBArgs        a{};
+    a.x = x; a.M = M; a.N = N;
+    a.q_row = static_cast<uint8_t *>(q_row); a.s_row = s_row_t;
+    a.q_col = static_cast<uint8_t *>(q_col_pad); a.s_col = s_col_pad;
+    a.group_offs = group_offs; a.padded_offs = vk_offs; a.G = G;
+    dim3 grid(static_cast<uint32_t>(cdiv(M_pad_max, TILE)), static_cast<uint32_t>(cdiv(N, TILE)), 1);
+    const bool v = vec_ok(x, in_dtype, N, {q_row, q_col_pad});
+    return launch_tile<QB_ROW | QB_COL | QB_SEGMENT>(a, in_dtype, fmt, grid, v, st);
+}
+
+extern "C" int pta_grouped_compute_padded_offs(const int64_t *offs, int64_t *padded_offs, int64_t G,
+                                               int64_t align, pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(offs && padded_offs && G >= 0 && align >= 1, "bad arguments");
+    offs_to_padded_offs_kernel<<<1, 256, 0, as_stream(stream)>>>(offs, padded_offs, G, align);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+extern "C" int pta_grouped_compute_offs(const int64_t *lens, int64_t *offs, int64_t G,
+                                        pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(lens && offs && G >= 0, "bad arguments");
+    padded_offs_kernel<<<1, 256, 0, as_stream(stream)>>>(lens, nullptr, offs, G, 1);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}

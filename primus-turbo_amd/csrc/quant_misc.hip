@@ -1,0 +1,667 @@
+// Tensorwise / rowwise / MXFP8 quantization, dequantization and byte
+// transposes for gfx950.
+//
+// Scale arithmetic follows the reference's HIP kernels:
+//   amax -> scale, eps 1e-12  csrc/include/primus_turbo/device/quant_utils.cuh:53-72
+//   quant op                  csrc/include/primus_turbo/device/quant_utils.cuh:31-38
+//   rowwise (row-major)       csrc/kernels/quantization/quantization_rowwise.cu:57-135
+//   rowwise (other axis)      csrc/kernels/quantization/quantization_rowwise.cu:186-235
+// The MX rule (kernel source absent from the reference snapshot) is the OCP
+// MX v1.0 shared-exponent rule encoded by the constants of
+// csrc/include/primus_turbo/quantization.h:88-102:
+//   e8m0 = clamp(biased_exp(amax) - emax_elem, 0, 254), q = fp8(x * 2^(127 - e8m0)).
+#include "common.h"
+
+namespace pta {
+namespace {
+
+constexpr int NT = 256;
+
+// ---------------------------------------------------------------------------
+// TENSORWISE
+// ---------------------------------------------------------------------------
+constexpr int TW_MAX_PARTS = 2048;
+
+// pass 1: per-block partial amax (16 elements per lane per iteration)
+template <int IN_DT, bool VEC>
+__global__ __launch_bounds__(NT) void tw_amax_kernel(const void *x, int64_t n, float *partial) {
+    float         a      = 0.0f;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * NT * 16;
+    for (int64_t base = (static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x) * 16; base < n;
+         base += stride) {
+        if (VEC && base + 16 <= n) {
+            float v[8], w[8];
+            load8<IN_DT>(x, base, v);
+            load8<IN_DT>(x, base + 8, w);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a = fmaxf(a, fmaxf(fabsf(v[j]), fabsf(w[j])));
+        } else {
+            for (int j = 0; j < 16; ++j)
+                if (base + j < n) a = fmaxf(a, fabsf(load_scalar<IN_DT>(x, base + j)));
+        }
+    }
+    a = max64(a);
+    __shared__ float s[NT / 64];
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+}
+
+// pass 2: every block reduces the partials (tiny, L2-resident), then quantizes
+template <int IN_DT, int FMT, bool VEC>
+__global__ __launch_bounds__(NT) void tw_quant_kernel(const void *x, int64_t n, const float *partial,
+                                                       int nparts, const float *scale_in,
+                                                       uint8_t *q, float *scale_inv) {
+    __shared__ float s_scale;
+    if (threadIdx.x < 64) {
+        float sc;
+        if (scale_in != nullptr) {
+            sc = scale_in[0];
+        } else {
+            float a = 0.0f;
+            for (int i = threadIdx.x; i < nparts; i += 64) a = fmaxf(a, partial[i]);
+            a  = max64(a);
+            sc = scale_from_amax<FMT>(a, 1e-12f);
+        }
+        if (threadIdx.x == 0) {
+            s_scale = sc;
+            if (blockIdx.x == 0) scale_inv[0] = 1.0f / sc;
+        }
+    }
+    __syncthreads();
+    const float   sc     = s_scale;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * NT * 16;
+    for (int64_t base = (static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x) * 16; base < n;
+         base += stride) {
+        if (VEC && base + 16 <= n) {
+            float v[16];
+            float a[8], b[8];
+            load8<IN_DT>(x, base, a);
+            load8<IN_DT>(x, base + 8, b);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) { v[j] = a[j]; v[j + 8] = b[j]; }
+            *reinterpret_cast<uint4 *>(q + base) =
+                make_uint4(quant4<FMT>(v, sc), quant4<FMT>(v + 4, sc), quant4<FMT>(v + 8, sc),
+                           quant4<FMT>(v + 12, sc));
+        } else {
+            for (int j = 0; j < 16; ++j)
+                if (base + j < n) q[base + j] = cvt1_fp8<FMT>(qclamp<FMT>(load_scalar<IN_DT>(x, base + j), sc));
+        }
+    }
+}
+
+int tw_grid(int64_t n) {
+    int64_t g = cdiv(n, static_cast<int64_t>(NT) * 16 * 4);
+    if (g < 1) g = 1;
+    if (g > TW_MAX_PARTS) g = TW_MAX_PARTS;
+    return static_cast<int>(g);
+}
+
+// ---------------------------------------------------------------------------
+// ROWWISE along the last axis: one wave per row (len <= 4096) or one
+// workgroup per row (len <= 16384); values stay in VGPRs (single HBM read).
+// Longer rows fall back to two sweeps of the row.
+// ---------------------------------------------------------------------------
+template <int IN_DT, int FMT, bool VEC, int CPT, bool WAVE_PER_ROW>
+__global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows, int64_t len,
+                                                      const float *scale_in, uint8_t *q,
+                                                      float *scale_inv) {
+    constexpr int LANES = WAVE_PER_ROW ? 64 : NT;
+    const int64_t row   = WAVE_PER_ROW ? static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)
+                                       : static_cast<int64_t>(blockIdx.x);
+    const int     l     = WAVE_PER_ROW ? (threadIdx.x & 63) : threadIdx.x;
+    if (WAVE_PER_ROW && row >= rows) return; // whole wave exits together
+    const int64_t off = row * len;
+
+    float v[CPT][16];
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int64_t base = (static_cast<int64_t>(c) * LANES + l) * 16;
+        if (VEC && base + 16 <= len) {
+            float p[8], r[8];
+            load8<IN_DT>(x, off + base, p);
+            load8<IN_DT>(x, off + base + 8, r);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) { v[c][j] = p[j]; v[c][j + 8] = r[j]; }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[c][j] = base + j < len ? load_scalar<IN_DT>(x, off + base + j) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[c][j]));
+    }
+    float sc;
+    if (scale_in != nullptr) {
+        sc = scale_in[row];
+    } else {
+        a = max64(a);
+        if constexpr (!WAVE_PER_ROW) {
+            __shared__ float s[NT / 64];
+            if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = a;
+            __syncthreads();
+            a = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        }
+        sc = scale_from_amax<FMT>(a, 1e-12f);
+    }
+    if (l == 0) scale_inv[row] = 1.0f / sc;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int64_t base = (static_cast<int64_t>(c) * LANES + l) * 16;
+        if (VEC && base + 16 <= len) {
+            *reinterpret_cast<uint4 *>(q + off + base) =
+                make_uint4(quant4<FMT>(&v[c][0], sc), quant4<FMT>(&v[c][4], sc),
+                           quant4<FMT>(&v[c][8], sc), quant4<FMT>(&v[c][12], sc));
+        } else {
+            for (int j = 0; j < 16; ++j)
+                if (base + j < len) q[off + base + j] = cvt1_fp8<FMT>(qclamp<FMT>(v[c][j], sc));
+        }
+    }
+}
+
+template <int IN_DT, int FMT>
+__global__ __launch_bounds__(NT) void rw_last_long_kernel(const void *x, int64_t len,
+                                                           const float *scale_in, uint8_t *q,
+                                                           float *scale_inv) {
+    const int64_t row = blockIdx.x;
+    const int64_t off = row * len;
+    float         sc;
+    if (scale_in != nullptr) {
+        sc = scale_in[row];
+    } else {
+        float a = 0.0f;
+        for (int64_t i = threadIdx.x; i < len; i += NT) a = fmaxf(a, fabsf(load_scalar<IN_DT>(x, off + i)));
+        a = max64(a);
+        __shared__ float s[NT / 64];
+        if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = a;
+        __syncthreads();
+        a  = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        sc = scale_from_amax<FMT>(a, 1e-12f);
+    }
+    if (threadIdx.x == 0) scale_inv[row] = 1.0f / sc;
+    for (int64_t i = threadIdx.x; i < len; i += NT)
+        q[off + i] = cvt1_fp8<FMT>(qclamp<FMT>(load_scalar<IN_DT>(x, off + i), sc));
+}
+
+// ---------------------------------------------------------------------------
+// ROWWISE along a non-last axis: x[outer, len, inner] -> scale per (o, n).
+// pass 1: partial column amax over chunks of RW_CH rows;
+// pass 2: finalize scale / scale_inv per column;
+// pass 3: quantize.
+// ---------------------------------------------------------------------------
+constexpr int RW_CH = 64;
+
+template <int IN_DT>
+__global__ __launch_bounds__(NT) void rw_col_partial_kernel(const void *x, int64_t len, int64_t inner,
+                                                             float *partial, int64_t nchunk) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+    const int64_t c = blockIdx.y, o = blockIdx.z;
+    if (n >= inner) return;
+    const int64_t r0 = c * RW_CH, r1 = r0 + RW_CH < len ? r0 + RW_CH : len;
+    float         a  = 0.0f;
+    for (int64_t r = r0; r < r1; ++r) a = fmaxf(a, fabsf(load_scalar<IN_DT>(x, (o * len + r) * inner + n)));
+    partial[(o * nchunk + c) * inner + n] = a;
+}
+
+template <int FMT>
+__global__ __launch_bounds__(NT) void rw_col_finalize_kernel(const float *partial, int64_t nchunk,
+                                                              int64_t inner, const float *scale_in,
+                                                              float *scale, float *scale_inv) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+    const int64_t o = blockIdx.y;
+    if (n >= inner) return;
+    float sc;
+    if (scale_in != nullptr) {
+        sc = scale_in[o * inner + n];
+    } else {
+        float a = 0.0f;
+        for (int64_t c = 0; c < nchunk; ++c) a = fmaxf(a, partial[(o * nchunk + c) * inner + n]);
+        sc = scale_from_amax<FMT>(a, 1e-12f);
+    }
+    scale[o * inner + n]     = sc;
+    scale_inv[o * inner + n] = 1.0f / sc;
+}
+
+template <int IN_DT, int FMT>
+__global__ __launch_bounds__(NT) void rw_col_quant_kernel(const void *x, int64_t len, int64_t inner,
+                                                           const float *scale, uint8_t *q) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+    const int64_t c = blockIdx.y, o = blockIdx.z;
+    if (n >= inner) return;
+    const float   sc = scale[o * inner + n];
+    const int64_t r0 = c * RW_CH, r1 = r0 + RW_CH < len ? r0 + RW_CH : len;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int64_t i = (o * len + r) * inner + n;
+        q[i]            = cvt1_fp8<FMT>(qclamp<FMT>(load_scalar<IN_DT>(x, i), sc));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MXFP8: tile of 64 rows x 64 cols per workgroup (input x[G, M, N]).
+// Rowwise: lane t owns row t>>2 ... using 4 lanes per 64-col row, 16 cols each.
+// Colwise: the tile is staged in LDS and lane t owns column t>>2, 16 rows.
+// ---------------------------------------------------------------------------
+template <int FMT> __device__ __forceinline__ int mx_e8m0(float amax) {
+    constexpr int emax = FMT == PTA_E4M3 ? 8 : 15;
+    const int     be   = static_cast<int>((__float_as_uint(amax) >> 23) & 0xffu);
+    int           e    = be - emax;
+    e                  = e < 0 ? 0 : (e > 254 ? 254 : e);
+    return amax > 0.0f ? e : 0;
+}
+__device__ __forceinline__ float mx_qscale(int e8m0) {
+    return __uint_as_float(static_cast<uint32_t>(254 - e8m0) << 23); // 2^(127 - e8m0)
+}
+
+template <int IN_DT, int FMT>
+__global__ __launch_bounds__(NT) void mx_quant_kernel(const void *x, int64_t M, int64_t N, int64_t M_pad,
+                                                       int64_t N_pad, uint8_t *q_row, uint8_t *e_row,
+                                                       int use2d_row, uint8_t *q_col, uint8_t *e_col,
+                                                       int use2d_col) {
+    const int     t  = threadIdx.x;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 64;
+    const int64_t g  = blockIdx.z;
+    const int64_t xoff = g * M * N;
+
+    __shared__ float s_tile[64][65];
+    __shared__ float s_bmax[2][2]; // 32x32 block maxima for the 2-D variant
+    // load: 64 rows x 64 cols, lane t: row t>>2 (+0 / +... ) handled in 4 passes of 16 rows
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int     rl = p * 16 + (t >> 4);
+        const int     cl = (t & 15) * 4;
+        const int64_t m = m0 + rl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n = n0 + cl + j;
+            s_tile[rl][cl + j] = (m < M && n < N) ? load_scalar<IN_DT>(x, xoff + m * N + n) : 0.0f;
+        }
+    }
+    if (t < 4) s_bmax[t >> 1][t & 1] = 0.0f;
+    __syncthreads();
+    const bool need2d = (q_row && use2d_row) || (q_col && use2d_col);
+    if (need2d) {
+        // lane t: row t>>2, 16 cols ((t&3)*16): contributes to block (row/32, col/32)
+        const int rl = t >> 2, cl = (t & 3) * 16;
+        float     a  = 0.0f;
+        for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(s_tile[rl][cl + j]));
+        // non-negative floats order like their bit patterns: integer max in LDS
+        atomicMax(reinterpret_cast<int *>(&s_bmax[rl >> 5][cl >> 5]), __float_as_int(a));
+        __syncthreads();
+    }
+    if (q_row != nullptr) {
+        // lane t: row t>>2, 16 cols; 32-col block = lanes pair (t, t^1)
+        const int     rl = t >> 2, cl = (t & 3) * 16;
+        const int64_t m  = m0 + rl;
+        float         v[16];
+        float         a = 0.0f;
+        for (int j = 0; j < 16; ++j) {
+            v[j] = s_tile[rl][cl + j];
+            a    = fmaxf(a, fabsf(v[j]));
+        }
+        a = fmaxf(a, dpp_f<PTA_DPP_QUAD_XOR1>(a));
+        if (use2d_row) a = s_bmax[rl >> 5][cl >> 5];
+        const int   e  = mx_e8m0<FMT>(a);
+        const float sc = mx_qscale(e);
+        if (m < M && n0 + cl < N_pad) {
+            uint8_t *dst = q_row + (g * M + m) * N_pad + n0 + cl;
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(v, sc), quant4<FMT>(v + 4, sc),
+                                                         quant4<FMT>(v + 8, sc), quant4<FMT>(v + 12, sc));
+            if ((t & 1) == 0) e_row[(g * M + m) * (N_pad / 32) + (n0 + cl) / 32] = static_cast<uint8_t>(e);
+        }
+    }
+    if (q_col != nullptr) {
+        // lane t: column t>>2, 16 rows ((t&3)*16); 32-row block = lanes pair (t, t^1)
+        const int     cl = t >> 2, rl = (t & 3) * 16;
+        const int64_t n  = n0 + cl;
+        float         v[16];
+        float         a = 0.0f;
+        for (int j = 0; j < 16; ++j) {
+            v[j] = s_tile[rl + j][cl];
+            a    = fmaxf(a, fabsf(v[j]));
+        }
+        a = fmaxf(a, dpp_f<PTA_DPP_QUAD_XOR1>(a));
+        if (use2d_col) a = s_bmax[rl >> 5][cl >> 5];
+        const int   e  = mx_e8m0<FMT>(a);
+        const float sc = mx_qscale(e);
+        if (n < N && m0 + rl < M_pad) {
+            uint8_t *dst = q_col + (g * N + n) * M_pad + m0 + rl;
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(v, sc), quant4<FMT>(v + 4, sc),
+                                                         quant4<FMT>(v + 8, sc), quant4<FMT>(v + 12, sc));
+            if ((t & 1) == 0) e_col[(g * N + n) * (M_pad / 32) + (m0 + rl) / 32] = static_cast<uint8_t>(e);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization kernels
+// ---------------------------------------------------------------------------
+template <int FMT> __device__ __forceinline__ float fp8_to_f32(uint32_t b) {
+    // exact decode of an OCP fp8 byte (gfx950 v_cvt_f32_fp8 / v_cvt_f32_bf8)
+    if constexpr (FMT == PTA_E4M3) return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(b), 0);
+    else return __builtin_amdgcn_cvt_f32_bf8(static_cast<int>(b), 0);
+}
+
+template <int OUT_DT> __device__ __forceinline__ void store_out(void *y, int64_t i, float v) {
+    if constexpr (OUT_DT == PTA_F32) reinterpret_cast<float *>(y)[i] = v;
+    else if constexpr (OUT_DT == PTA_BF16) reinterpret_cast<uint16_t *>(y)[i] = f32_to_bf16_bits(v);
+    else reinterpret_cast<uint16_t *>(y)[i] = f32_to_f16_bits(v);
+}
+
+// mode: 0 tensor, 1 rowwise [outer,len,inner], 2 block axis0, 3 block axis1, 4 block 2d, 5 mx
+struct DQArgs {
+    const uint8_t *q;
+    const float   *s;
+    const uint8_t *e;
+    void          *y;
+    int64_t        n;
+    int64_t        d0, d1, d2; // mode-specific dims
+    int64_t        block;
+    int            transpose_out;
+};
+
+template <int FMT, int OUT_DT, int MODE>
+__global__ __launch_bounds__(NT) void dequant_kernel(DQArgs a) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * NT;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x; i < a.n; i += stride) {
+        float sc;
+        if constexpr (MODE == 0) {
+            sc = a.s[0];
+        } else if constexpr (MODE == 1) { // [outer, len, inner]
+            const int64_t inner = a.d2, len = a.d1;
+            const int64_t o = i / (len * inner), nn = i % inner;
+            sc = a.s[o * inner + nn];
+        } else if constexpr (MODE == 2) { // [M, N], s[ceil(M/b), N]
+            const int64_t N = a.d1;
+            sc = a.s[(i / N) / a.block * N + (i % N)];
+        } else if constexpr (MODE == 3) { // [M, N], s[M, ceil(N/b)]
+            const int64_t N = a.d1, nb = (N + a.block - 1) / a.block;
+            sc = a.s[(i / N) * nb + (i % N) / a.block];
+        } else if constexpr (MODE == 4) { // [B, M, N], s[B, mb, nb]
+            const int64_t M = a.d1, N = a.d2;
+            const int64_t mb = (M + a.block - 1) / a.block, nb = (N + a.block - 1) / a.block;
+            const int64_t b = i / (M * N), r = (i / N) % M, c = i % N;
+            sc = a.s[(b * mb + r / a.block) * nb + c / a.block];
+        } else { // MX: q[R, C], e[R, C/32]
+            const int64_t C = a.d1;
+            const int64_t r = i / C, c = i % C;
+            sc = __uint_as_float(static_cast<uint32_t>(a.e[r * (C / 32) + c / 32]) << 23);
+        }
+        const float v = fp8_to_f32<FMT>(a.q[i]) * sc;
+        if constexpr (MODE == 5) {
+            if (a.transpose_out) {
+                const int64_t R = a.d0, C = a.d1;
+                store_out<OUT_DT>(a.y, (i % C) * R + i / C, v);
+                continue;
+            }
+        }
+        store_out<OUT_DT>(a.y, i, v);
+    }
+}
+
+template <int MODE> int launch_dequant(const DQArgs &a, int fmt, int out_dt, hipStream_t st) {
+    if (a.n == 0) return PTA_OK;
+    int64_t g = cdiv(a.n, NT);
+    if (g > 65536) g = 65536;
+    const dim3 grid(static_cast<uint32_t>(g));
+#define PTA_DQ(F, O) dequant_kernel<F, O, MODE><<<grid, NT, 0, st>>>(a)
+#define PTA_DQ_O(F)                                                                                \
+    if (out_dt == PTA_BF16) PTA_DQ(F, PTA_BF16);                                                   \
+    else if (out_dt == PTA_F16) PTA_DQ(F, PTA_F16);                                                \
+    else PTA_DQ(F, PTA_F32)
+    if (fmt == PTA_E4M3) { PTA_DQ_O(PTA_E4M3); }
+    else { PTA_DQ_O(PTA_E5M2); }
+#undef PTA_DQ_O
+#undef PTA_DQ
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// byte transpose x[B, M, N] -> y[B, N, M], 64 x 64 tiles
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NT) void transpose_u8_kernel(const uint8_t *x, int64_t M, int64_t N, uint8_t *y) {
+    __shared__ uint8_t s[64][68];
+    const int64_t b = blockIdx.z, m0 = static_cast<int64_t>(blockIdx.y) * 64, n0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const uint8_t *xb = x + b * M * N;
+    uint8_t       *yb = y + b * M * N;
+    const int      t  = threadIdx.x;
+    // read: 64 rows x 64 bytes; lane t: row t>>2, 16 bytes at (t&3)*16
+    {
+        const int     r = t >> 2, c = (t & 3) * 16;
+        const int64_t m = m0 + r;
+        for (int j = 0; j < 16; ++j) {
+            const int64_t n = n0 + c + j;
+            s[r][c + j] = (m < M && n < N) ? xb[m * N + n] : 0;
+        }
+    }
+    __syncthreads();
+    {
+        const int     r = t >> 2, c = (t & 3) * 16; // r: output row (n), c: output col (m)
+        const int64_t n = n0 + r;
+        if (n < N) {
+            for (int j = 0; j < 16; ++j) {
+                const int64_t m = m0 + c + j;
+                if (m < M) yb[n * M + m] = s[c + j][r];
+            }
+        }
+    }
+}
+
+template <int IN_DT, int FMT>
+int tw_launch(const void *x, int64_t n, const float *scale, uint8_t *q, float *scale_inv,
+              float *parts, bool vec, hipStream_t st) {
+    const int g = tw_grid(n);
+    if (scale == nullptr) {
+        if (vec) tw_amax_kernel<IN_DT, true><<<g, NT, 0, st>>>(x, n, parts);
+        else tw_amax_kernel<IN_DT, false><<<g, NT, 0, st>>>(x, n, parts);
+        PTA_CHECK_LAUNCH();
+    }
+    if (vec) tw_quant_kernel<IN_DT, FMT, true><<<g, NT, 0, st>>>(x, n, parts, g, scale, q, scale_inv);
+    else tw_quant_kernel<IN_DT, FMT, false><<<g, NT, 0, st>>>(x, n, parts, g, scale, q, scale_inv);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+template <int IN_DT, int FMT>
+int rw_last_launch(const void *x, int64_t rows, int64_t len, const float *scale, uint8_t *q,
+                   float *scale_inv, bool vec, hipStream_t st) {
+    const int64_t cpt64 = cdiv(len, 64 * 16);
+    if (cpt64 <= 4) {
+        const dim3 grid(static_cast<uint32_t>(cdiv(rows, 4)));
+#define PTA_RW_W(C)                                                                                \
+    if (vec) rw_last_kernel<IN_DT, FMT, true, C, true><<<grid, NT, 0, st>>>(x, rows, len, scale, q, scale_inv); \
+    else rw_last_kernel<IN_DT, FMT, false, C, true><<<grid, NT, 0, st>>>(x, rows, len, scale, q, scale_inv)
+        if (cpt64 == 1) { PTA_RW_W(1); }
+        else if (cpt64 == 2) { PTA_RW_W(2); }
+        else { PTA_RW_W(4); }
+#undef PTA_RW_W
+    } else if (cdiv(len, NT * 16) <= 4) {
+        const int64_t cpt = cdiv(len, NT * 16);
+        const dim3    grid(static_cast<uint32_t>(rows));
+#define PTA_RW_B(C)                                                                                \
+    if (vec) rw_last_kernel<IN_DT, FMT, true, C, false><<<grid, NT, 0, st>>>(x, rows, len, scale, q, scale_inv); \
+    else rw_last_kernel<IN_DT, FMT, false, C, false><<<grid, NT, 0, st>>>(x, rows, len, scale, q, scale_inv)
+        if (cpt <= 2) { PTA_RW_B(2); }
+        else { PTA_RW_B(4); }
+#undef PTA_RW_B
+    } else {
+        rw_last_long_kernel<IN_DT, FMT><<<static_cast<uint32_t>(rows), NT, 0, st>>>(x, len, scale, q, scale_inv);
+    }
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+template <int IN_DT, int FMT>
+int rw_col_launch(const void *x, int64_t outer, int64_t len, int64_t inner, const float *scale_in,
+                  uint8_t *q, float *scale_inv, float *ws, hipStream_t st) {
+    const int64_t nchunk  = cdiv(len, RW_CH);
+    float        *scale   = ws;
+    float        *partial = ws + outer * inner;
+    const dim3    g3(static_cast<uint32_t>(cdiv(inner, NT)), static_cast<uint32_t>(nchunk),
+                     static_cast<uint32_t>(outer));
+    if (scale_in == nullptr) {
+        rw_col_partial_kernel<IN_DT><<<g3, NT, 0, st>>>(x, len, inner, partial, nchunk);
+        PTA_CHECK_LAUNCH();
+    }
+    rw_col_finalize_kernel<FMT><<<dim3(static_cast<uint32_t>(cdiv(inner, NT)), static_cast<uint32_t>(outer)), NT, 0, st>>>(
+        partial, nchunk, inner, scale_in, scale, scale_inv);
+    PTA_CHECK_LAUNCH();
+    rw_col_quant_kernel<IN_DT, FMT><<<g3, NT, 0, st>>>(x, len, inner, scale, q);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+int check_in(const void *x, int in_dtype, int fmt) {
+    PTA_CHECK_ARG(x != nullptr, "input pointer is NULL");
+    PTA_CHECK_ARG(in_dtype == PTA_BF16 || in_dtype == PTA_F16 || in_dtype == PTA_F32,
+                  "unsupported input dtype code %d", in_dtype);
+    PTA_CHECK_ARG(fmt == PTA_E4M3 || fmt == PTA_E5M2, "unsupported fp8 format code %d", fmt);
+    return PTA_OK;
+}
+
+#define PTA_DISPATCH_IN_FMT(in_dtype, fmt, FN, ...)                                                \
+    [&]() -> int {                                                                                 \
+        if (in_dtype == PTA_BF16) return fmt == PTA_E4M3 ? FN<PTA_BF16, PTA_E4M3>(__VA_ARGS__)    \
+                                                         : FN<PTA_BF16, PTA_E5M2>(__VA_ARGS__);   \
+        if (in_dtype == PTA_F16) return fmt == PTA_E4M3 ? FN<PTA_F16, PTA_E4M3>(__VA_ARGS__)      \
+                                                        : FN<PTA_F16, PTA_E5M2>(__VA_ARGS__);     \
+        return fmt == PTA_E4M3 ? FN<PTA_F32, PTA_E4M3>(__VA_ARGS__) : FN<PTA_F32, PTA_E5M2>(__VA_ARGS__); \
+    }()
+
+template <int IN_DT, int FMT>
+int mx_launch(const void *x, int64_t G, int64_t M, int64_t N, uint8_t *q_row, uint8_t *e_row,
+              int u2r, uint8_t *q_col, uint8_t *e_col, int u2c, hipStream_t st) {
+    const int64_t M_pad = cdiv(M, 128) * 128, N_pad = cdiv(N, 128) * 128;
+    const dim3    grid(static_cast<uint32_t>(M_pad / 64), static_cast<uint32_t>(N_pad / 64),
+                       static_cast<uint32_t>(G));
+    mx_quant_kernel<IN_DT, FMT><<<grid, NT, 0, st>>>(x, M, N, M_pad, N_pad, q_row, e_row, u2r, q_col, e_col, u2c);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+} // namespace
+} // namespace pta
+
+using namespace pta;
+
+extern "C" size_t pta_quantize_fp8_tensorwise_workspace_size(int64_t) {
+    return TW_MAX_PARTS * sizeof(float);
+}
+
+extern "C" int pta_quantize_fp8_tensorwise(const void *x, int in_dtype, int64_t n, const float *scale,
+                                           void *q, int fmt, float *scale_inv, void *workspace,
+                                           size_t workspace_bytes, pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_in(x, in_dtype, fmt)) return rc;
+    PTA_CHECK_ARG(q && scale_inv && n >= 0, "bad arguments");
+    PTA_CHECK_ARG(scale != nullptr || (workspace && workspace_bytes >= TW_MAX_PARTS * sizeof(float)),
+                  "workspace of %zu bytes required", (size_t)(TW_MAX_PARTS * sizeof(float)));
+    const bool vec = aligned16(x) && aligned16(q);
+    return PTA_DISPATCH_IN_FMT(in_dtype, fmt, tw_launch, x, n, scale, static_cast<uint8_t *>(q),
+                               scale_inv, static_cast<float *>(workspace), vec, as_stream(stream));
+}
+
+extern "C" size_t pta_quantize_fp8_rowwise_workspace_size(int64_t outer, int64_t len, int64_t inner) {
+    if (inner == 1) return 0;
+    return static_cast<size_t>(outer * inner * (1 + cdiv(len, RW_CH))) * sizeof(float);
+}
+
+extern "C" int pta_quantize_fp8_rowwise(const void *x, int in_dtype, int64_t outer, int64_t len,
+                                        int64_t inner, const float *scale, void *q, int fmt,
+                                        float *scale_inv, void *workspace, size_t workspace_bytes,
+                                        pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_in(x, in_dtype, fmt)) return rc;
+    PTA_CHECK_ARG(q && scale_inv && outer >= 0 && len >= 0 && inner >= 1, "bad arguments");
+    if (outer == 0 || len == 0) return PTA_OK;
+    hipStream_t st = as_stream(stream);
+    if (inner == 1) {
+        PTA_CHECK_ARG(outer <= 0x7fffffffLL, "too many rows");
+        const bool vec = aligned16(x) && aligned16(q) && (len % 16 == 0);
+        return PTA_DISPATCH_IN_FMT(in_dtype, fmt, rw_last_launch, x, outer, len, scale,
+                                   static_cast<uint8_t *>(q), scale_inv, vec, st);
+    }
+    const size_t need = pta_quantize_fp8_rowwise_workspace_size(outer, len, inner);
+    PTA_CHECK_ARG(workspace && workspace_bytes >= need, "workspace of %zu bytes required", need);
+    PTA_CHECK_ARG(outer <= 65535 && cdiv(len, RW_CH) <= 65535, "shape too large");
+    return PTA_DISPATCH_IN_FMT(in_dtype, fmt, rw_col_launch, x, outer, len, inner, scale,
+                               static_cast<uint8_t *>(q), scale_inv,
+                               static_cast<float *>(workspace), st);
+}
+
+extern "C" int pta_quantize_mxfp8(const void *x, int in_dtype, int64_t G, int64_t M, int64_t N,
+                                  void *q_row, uint8_t *e_row, int use_2d_row, void *q_col,
+                                  uint8_t *e_col, int use_2d_col, int fmt, pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_in(x, in_dtype, fmt)) return rc;
+    PTA_CHECK_ARG(in_dtype != PTA_F32, "MXFP8 quantization takes bf16 or fp16 input");
+    PTA_CHECK_ARG(G >= 1 && M >= 0 && N >= 0 && G <= 65535, "bad shape");
+    PTA_CHECK_ARG(N % 32 == 0, "N must be divisible by 32");
+    PTA_CHECK_ARG((q_row == nullptr) == (e_row == nullptr), "q_row/e_row must both be set or NULL");
+    PTA_CHECK_ARG((q_col == nullptr) == (e_col == nullptr), "q_col/e_col must both be set or NULL");
+    PTA_CHECK_ARG(q_row || q_col, "no output requested");
+    PTA_CHECK_ARG((!q_row || aligned16(q_row)) && (!q_col || aligned16(q_col)), "outputs must be 16-byte aligned");
+    if (M == 0 || N == 0) return PTA_OK;
+    return PTA_DISPATCH_IN_FMT(in_dtype, fmt, mx_launch, x, G, M, N, static_cast<uint8_t *>(q_row),
+                               e_row, use_2d_row, static_cast<uint8_t *>(q_col), e_col, use_2d_col,
+                               as_stream(stream));
+}
+
+extern "C" int pta_dequantize_fp8_tensorwise(const void *q, int fmt, int64_t n, const float *scale_inv,
+                                             void *y, int out_dtype, pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(q && y && scale_inv && n >= 0, "bad arguments");
+    DQArgs a{};
+    a.q = static_cast<const uint8_t *>(q); a.s = scale_inv; a.y = y; a.n = n;
+    return launch_dequant<0>(a, fmt, out_dtype, as_stream(stream));
+}
+
+extern "C" int pta_dequantize_fp8_rowwise(const void *q, int fmt, int64_t outer, int64_t len,
+                                          int64_t inner, const float *scale_inv, void *y,
+                                          int out_dtype, pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(q && y && scale_inv && outer >= 0 && len >= 0 && inner >= 1, "bad arguments");
+    DQArgs a{};
+    a.q = static_cast<const uint8_t *>(q); a.s = scale_inv; a.y = y;
+    a.n = outer * len * inner; a.d0 = outer; a.d1 = len; a.d2 = inner;
+    return launch_dequant<1>(a, fmt, out_dtype, as_stream(stream));
+}
+
+extern "C" int pta_dequantize_fp8_blockwise(const void *q, int fmt, int64_t B, int64_t M, int64_t N,
+                                            int64_t block, int mode, const float *scale_inv, void *y,
+                                            int out_dtype, pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(q && y && scale_inv && B >= 1 && M >= 0 && N >= 0 && block > 0, "bad arguments");
+    DQArgs a{};
+    a.q = static_cast<const uint8_t *>(q); a.s = scale_inv; a.y = y; a.block = block;
+    a.n = B * M * N; a.d0 = B; a.d1 = M; a.d2 = N;
+    hipStream_t st = as_stream(stream);
+    if (mode == 0) { a.d1 = N; return launch_dequant<2>(a, fmt, out_dtype, st); }
+    if (mode == 1) { a.d1 = N; return launch_dequant<3>(a, fmt, out_dtype, st); }
+    PTA_CHECK_ARG(mode == 2, "mode must be 0, 1 or 2");
+    return launch_dequant<4>(a, fmt, out_dtype, st);
+}
+
+extern "C" int pta_dequantize_mxfp8(const void *q, int fmt, int64_t R, int64_t C, const uint8_t *e8m0,
+                                    int transpose_out, void *y, int out_dtype, pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(q && y && e8m0 && R >= 0 && C >= 0 && C % 32 == 0, "bad arguments");
+    DQArgs a{};
+    a.q = static_cast<const uint8_t *>(q); a.e = e8m0; a.y = y;
+    a.n = R * C; a.d0 = R; a.d1 = C; a.transpose_out = transpose_out;
+    return launch_dequant<5>(a, fmt, out_dtype, as_stream(stream));
+}
+
+extern "C" int pta_transpose_u8(const void *x, int64_t B, int64_t M, int64_t N, void *y,
+                                pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(x && y && B >= 1 && M >= 0 && N >= 0 && B <= 65535, "bad arguments");
+    if (M == 0 || N == 0) return PTA_OK;
+    const dim3 grid(static_cast<uint32_t>(cdiv(N, 64)), static_cast<uint32_t>(cdiv(M, 64)),
+                    static_cast<uint32_t>(B));
+    transpose_u8_kernel<<<grid, NT, 0, as_stream(stream)>>>(static_cast<const uint8_t *>(x), M, N,
+                                                            static_cast<uint8_t *>(y));
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}

@@ -1,0 +1,148 @@
+"""ctypes binding of ``libprimus_turbo_amd.so`` (C ABI: include/primus_turbo_amd.h).
+
+The library is the only compute path: if it is missing, or no GPU is present,
+every op raises.  There is no CPU or eager-PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "lib", "libprimus_turbo_amd.so")
+
+PTA_F32, PTA_F16, PTA_BF16 = 0, 1, 2
+PTA_E4M3, PTA_E5M2 = 0, 1
+PTA_TENSORWISE, PTA_ROWWISE, PTA_BLOCKWISE, PTA_MX_BLOCKWISE = 1, 2, 3, 4
+
+_vp, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/primus_turbo_amd.h
+SIGNATURES = {
+    "pta_last_error": (ctypes.c_char_p, []),
+    "pta_abi_version": (_i32, []),
+    "pta_quantize_fp8_tensorwise_workspace_size": (_sz, [_i64]),
+    "pta_quantize_fp8_tensorwise": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
+    "pta_quantize_fp8_rowwise_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "pta_quantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
+    "pta_quantize_fp8_blockwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),
+    "pta_quantize_fp8_blockwise_dual": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
+    "pta_quantize_fp8_blockwise_for_weight": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp]),
+    "pta_quantize_fp8_blockwise_segment_m_row_col": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp],
+    ),
+    "pta_quantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp]),
+    "pta_dequantize_fp8_tensorwise": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp]),
+    "pta_dequantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp]),
+    "pta_dequantize_fp8_blockwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),
+    "pta_dequantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _vp, _i32, _vp]),
+    "pta_transpose_u8": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),
+    "pta_grouped_compute_offs": (_i32, [_vp, _vp, _i64, _vp]),
+    "pta_grouped_compute_padded_offs": (_i32, [_vp, _vp, _i64, _i64, _vp]),
+    "pta_gemm_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
+    "pta_gemm_fp8": (
+        _i32,
+        [_vp, _i32, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _i32, _i32, _i64, _i64, _i64, _i32, _vp, _sz, _vp],
+    ),
+    "pta_gemm_fp8_nt_strided": (
+        _i32,
+        [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i64, _i64, _i64, _i64, _i32,
+         _vp, _i64, _i64, _i32, _i64, _vp, _i64, _i64, _i32, _i64, _vp],
+    ),
+    "pta_grouped_gemm_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32]),
+    "pta_grouped_gemm_fp8": (
+        _i32,
+        [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+    "pta_grouped_gemm_fp8_variable_k_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
+    "pta_grouped_gemm_fp8_variable_k": (
+        _i32,
+        [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib_path() -> str:
+    return _LIB_PATH
+
+
+def load():
+    """Load the native library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(_LIB_PATH):
+                raise RuntimeError(
+                    f"primus_turbo native library not found at {_LIB_PATH}; build it with "
+                    "`make -C primus-turbo_amd` (or __graft_entry__.build())"
+                )
+            lib = ctypes.CDLL(_LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point and raise RuntimeError on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.pta_last_error().decode("utf-8", "replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream(device=None) -> int:
+    if not torch.cuda.is_available():
+        raise RuntimeError("primus_turbo FP8 ops need a ROCm GPU (torch.cuda.is_available() is False)")
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def in_dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return PTA_BF16
+    if dt == torch.float16:
+        return PTA_F16
+    if dt == torch.float32:
+        return PTA_F32
+    raise TypeError(f"unsupported high-precision dtype {dt}")
+
+
+def fp8_code(dt: torch.dtype) -> int:
+    if dt == torch.float8_e4m3fn:
+        return PTA_E4M3
+    if dt == torch.float8_e5m2:
+        return PTA_E5M2
+    raise TypeError(f"unsupported fp8 dtype {dt} (gfx950 uses OCP float8_e4m3fn / float8_e5m2)")
+
+
+def out_dtype_code(dt: torch.dtype) -> int:
+    return in_dtype_code(dt)
+
+
+def workspace(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes <= 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)

@@ -1,0 +1,365 @@
+"""Quantization impls: allocate outputs with torch, launch the gfx950 kernels.
+
+Function names, argument meaning and output layouts follow the reference's
+primus_turbo/pytorch/kernels/quantization/quantization_impl.py and the native
+ops of csrc/pytorch/quantization/quantization.cpp.  Every call goes through
+``libprimus_turbo_amd.so``; there is no fallback path.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from primus_turbo.pytorch import _C
+from primus_turbo.pytorch.core.low_precision import (
+    MXFP8_BLOCK_SIZE,
+    MXFP8_PADDING_ALIGN_SIZE,
+    ScalingRecipe,
+)
+
+
+def ceil_div(a: int, b: int) -> int:
+    return (a + b - 1) // b
+
+
+def _check_hp(x: torch.Tensor):
+    assert x.is_cuda, "input must be a GPU tensor"
+    assert x.dtype in (torch.bfloat16, torch.float16, torch.float32), f"unsupported input dtype {x.dtype}"
+
+
+# ---------------------------------------------------------------------------
+# tensorwise / rowwise  (quantization.cpp:42-206)
+# ---------------------------------------------------------------------------
+def quantize_fp8_tensorwise_impl(
+    x: torch.Tensor, out_dtype: torch.dtype, scale: Optional[torch.Tensor] = None
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    _check_hp(x)
+    x = x.contiguous()
+    q = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    scale_inv = torch.empty((), dtype=torch.float32, device=x.device)
+    ws = None
+    if scale is None:
+        ws = _C.workspace(_C.query("pta_quantize_fp8_tensorwise_workspace_size", x.numel()), x.device)
+    else:
+        assert scale.numel() == 1, "tensorwise scale must be scalar tensor"
+        scale = scale.to(torch.float32).contiguous()
+    _C.call(
+        "pta_quantize_fp8_tensorwise", _C.ptr(x), _C.in_dtype_code(x.dtype), x.numel(), _C.ptr(scale),
+        _C.ptr(q), _C.fp8_code(out_dtype), _C.ptr(scale_inv), _C.ptr(ws), 0 if ws is None else ws.numel(),
+        _C.stream(x.device),
+    )
+    return q, scale_inv
+
+
+def quantize_fp8_rowwise_impl(
+    x: torch.Tensor, out_dtype: torch.dtype, axis: int, scale: Optional[torch.Tensor] = None
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    _check_hp(x)
+    assert x.is_contiguous(), "The x tensor must be contiguous."
+    assert axis is not None, "axis must be specified for rowwise quantization"
+    nd = x.dim()
+    ax = axis if axis >= 0 else axis + nd
+    assert 0 <= ax < nd, f"axis {axis} out of range for a {nd}-D tensor"
+    shape = list(x.shape)
+    outer = 1
+    for s in shape[:ax]:
+        outer *= s
+    length = shape[ax]
+    inner = 1
+    for s in shape[ax + 1 :]:
+        inner *= s
+    sshape = list(shape)
+    sshape[ax] = 1
+    q = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    scale_inv = torch.empty(sshape, dtype=torch.float32, device=x.device)
+    if scale is not None:
+        assert list(scale.shape) == sshape, "rowwise scale shape mismatch"
+        scale = scale.to(torch.float32).contiguous()
+    ws = _C.workspace(_C.query("pta_quantize_fp8_rowwise_workspace_size", outer, length, inner), x.device)
+    _C.call(
+        "pta_quantize_fp8_rowwise", _C.ptr(x), _C.in_dtype_code(x.dtype), outer, length, inner, _C.ptr(scale),
+        _C.ptr(q), _C.fp8_code(out_dtype), _C.ptr(scale_inv), _C.ptr(ws), 0 if ws is None else ws.numel(),
+        _C.stream(x.device),
+    )
+    return q, scale_inv
+
+
+def dequantize_fp8_tensorwise_impl(x: torch.Tensor, out_dtype: torch.dtype, scale_inv: torch.Tensor):
+    x = x.contiguous()
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    s = scale_inv.to(torch.float32).contiguous()
+    _C.call(
+        "pta_dequantize_fp8_tensorwise", _C.ptr(x), _C.fp8_code(x.dtype), x.numel(), _C.ptr(s), _C.ptr(y),
+        _C.out_dtype_code(out_dtype), _C.stream(x.device),
+    )
+    return y
+
+
+def dequantize_fp8_rowwise_impl(x: torch.Tensor, out_dtype: torch.dtype, axis: int, scale_inv: torch.Tensor):
+    assert x.is_contiguous(), "The x tensor must be contiguous."
+    assert scale_inv.is_contiguous(), "The scale_inv tensor must be contiguous."
+    nd = x.dim()
+    ax = axis if axis >= 0 else axis + nd
+    shape = list(x.shape)
+    outer = 1
+    for s in shape[:ax]:
+        outer *= s
+    inner = 1
+    for s in shape[ax + 1 :]:
+        inner *= s
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    _C.call(
+        "pta_dequantize_fp8_rowwise", _C.ptr(x), _C.fp8_code(x.dtype), outer, shape[ax], inner,
+        _C.ptr(scale_inv), _C.ptr(y), _C.out_dtype_code(out_dtype), _C.stream(x.device),
+    )
+    return y
+
+
+# ---------------------------------------------------------------------------
+# blockwise  (quantization_impl.py:74-486)
+# ---------------------------------------------------------------------------
+def quant_fp8_blockwise_impl(
+    x: torch.Tensor, dtype: torch.dtype, axis: int, block_size: int = 128
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    _check_hp(x)
+    assert x.is_contiguous() and x.dim() == 2, "Input must be 2D and contiguous"
+    assert axis in (-2, -1, 0, 1), f"axis must be 0 or 1 (or -1, -2), got {axis}"
+    axis = axis % 2
+    M, N = x.shape
+    q = torch.empty((M, N), dtype=dtype, device=x.device)
+    sshape = (M, ceil_div(N, block_size)) if axis == 1 else (ceil_div(M, block_size), N)
+    s = torch.empty(sshape, dtype=torch.float32, device=x.device)
+    _C.call(
+        "pta_quantize_fp8_blockwise", _C.ptr(x), _C.in_dtype_code(x.dtype), M, N, block_size, axis, _C.ptr(q),
+        _C.ptr(s), _C.fp8_code(dtype), _C.stream(x.device),
+    )
+    return q, s
+
+
+def quant_fp8_blockwise_dual_impl(
+    x: torch.Tensor, dtype: torch.dtype, block_size: int = 128, col_transposed: bool = False
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Row (1 x bs) and column (bs x 1) quantization in one read of ``x``.
+
+    ``col_transposed=True`` (an extension used by the autograd functions) writes
+    the column-quantized bytes as ``[N, roundup(M, 128)]`` (zero padded) so the
+    wgrad GEMM reads them K-contiguously; the default is the reference's ``[M, N]``.
+    """
+    _check_hp(x)
+    assert x.is_contiguous() and x.dim() == 2, "Input must be 2D and contiguous"
+    M, N = x.shape
+    q_row = torch.empty((M, N), dtype=dtype, device=x.device)
+    s_row = torch.empty((M, ceil_div(N, block_size)), dtype=torch.float32, device=x.device)
+    q_col = torch.empty((N, ceil_div(M, 128) * 128) if col_transposed else (M, N), dtype=dtype, device=x.device)
+    s_col = torch.empty((ceil_div(M, block_size), N), dtype=torch.float32, device=x.device)
+    _C.call(
+        "pta_quantize_fp8_blockwise_dual", _C.ptr(x), _C.in_dtype_code(x.dtype), M, N, block_size, _C.ptr(q_row),
+        _C.ptr(s_row), _C.ptr(q_col), _C.ptr(s_col), int(col_transposed), _C.fp8_code(dtype), _C.stream(x.device),
+    )
+    return q_row, s_row, q_col, s_col
+
+
+def quant_fp8_blockwise_for_weight_impl(
+    w: torch.Tensor, dtype: torch.dtype, block_size: int = 128, with_transpose: bool = False
+):
+    """128 x 128 weight blocks; returns (q, s) or (q, s, q_t) with ``with_transpose``
+    (q_t: the same bytes as [B, N, roundup(M, 128)], zero padded)."""
+    _check_hp(w)
+    assert w.dim() in (2, 3)
+    w = w.contiguous()
+    squeeze = w.dim() == 2
+    B, M, N = (1, *w.shape) if squeeze else tuple(w.shape)
+    q = torch.empty((B, M, N), dtype=dtype, device=w.device)
+    s = torch.empty((B, ceil_div(M, block_size), ceil_div(N, block_size)), dtype=torch.float32, device=w.device)
+    q_t = torch.empty((B, N, ceil_div(M, 128) * 128), dtype=dtype, device=w.device) if with_transpose else None
+    _C.call(
+        "pta_quantize_fp8_blockwise_for_weight", _C.ptr(w), _C.in_dtype_code(w.dtype), B, M, N, block_size,
+        _C.ptr(q), _C.ptr(s), _C.ptr(q_t), _C.fp8_code(dtype), _C.stream(w.device),
+    )
+    if squeeze:
+        q, s = q[0], s[0]
+        q_t = q_t[0] if q_t is not None else None
+    if with_transpose:
+        return q, s, q_t
+    return q, s
+
+
+def dequant_fp8_blockwise_impl(
+    x_fp8: torch.Tensor, scale_inv: torch.Tensor, out_dtype: torch.dtype, axis: int, block_size: int = 128
+) -> torch.Tensor:
+    assert x_fp8.dim() == 2, "Input must be 2D"
+    x_fp8 = x_fp8.contiguous()
+    M, N = x_fp8.shape
+    out = torch.empty((M, N), dtype=out_dtype, device=x_fp8.device)
+    _C.call(
+        "pta_dequantize_fp8_blockwise", _C.ptr(x_fp8), _C.fp8_code(x_fp8.dtype), 1, M, N, block_size, axis % 2,
+        _C.ptr(scale_inv.contiguous()), _C.ptr(out), _C.out_dtype_code(out_dtype), _C.stream(x_fp8.device),
+    )
+    return out
+
+
+def dequant_fp8_blockwise_for_weight_impl(
+    w_fp8: torch.Tensor, scale_inv: torch.Tensor, out_dtype: torch.dtype, block_size: int = 128
+) -> torch.Tensor:
+    assert w_fp8.dim() in (2, 3)
+    w_fp8 = w_fp8.contiguous()
+    B, M, N = (1, *w_fp8.shape) if w_fp8.dim() == 2 else tuple(w_fp8.shape)
+    out = torch.empty(w_fp8.shape, dtype=out_dtype, device=w_fp8.device)
+    _C.call(
+        "pta_dequantize_fp8_blockwise", _C.ptr(w_fp8), _C.fp8_code(w_fp8.dtype), B, M, N, block_size, 2,
+        _C.ptr(scale_inv.contiguous()), _C.ptr(out), _C.out_dtype_code(out_dtype), _C.stream(w_fp8.device),
+    )
+    return out
+
+
+def quant_fp8_blockwise_segment_m_row_col_impl(
+    x: torch.Tensor,
+    dtype: torch.dtype,
+    block_size: int,
+    group_lens: torch.Tensor,
+    group_offs: torch.Tensor,
+    gemm_other_dim: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused row + segment-padded column quantization of a grouped tensor.
+
+    Returns (x_fp8_row [M,N], x_fp8_col_padded [M+G*bs, N], x_scales_row [N/bs, M],
+    x_scales_col_padded [(M+G*bs)/bs, N], var_k_group_lens [G], var_k_group_offs [G+1]).
+    ``gemm_other_dim`` is accepted for signature compatibility; one kernel serves all sizes.
+    """
+    _check_hp(x)
+    assert x.is_contiguous() and x.dim() == 2
+    M, N = x.shape
+    G = group_lens.size(0)
+    Mpad = M + G * block_size
+    dev = x.device
+    q_row = torch.empty((M, N), dtype=dtype, device=dev)
+    q_col = torch.empty((Mpad, N), dtype=dtype, device=dev)
+    s_row = torch.empty((ceil_div(N, block_size), M), dtype=torch.float32, device=dev)
+    s_col = torch.empty((ceil_div(Mpad, block_size), N), dtype=torch.float32, device=dev)
+    vk_lens = torch.empty(G, dtype=torch.int64, device=dev)
+    vk_offs = torch.empty(G + 1, dtype=torch.int64, device=dev)
+    _C.call(
+        "pta_quantize_fp8_blockwise_segment_m_row_col", _C.ptr(x), _C.in_dtype_code(x.dtype), M, N, G,
+        _C.ptr(group_lens.contiguous()), _C.ptr(group_offs.contiguous()), block_size, _C.ptr(q_row), _C.ptr(q_col),
+        _C.ptr(s_row), _C.ptr(s_col), _C.ptr(vk_lens), _C.ptr(vk_offs), _C.fp8_code(dtype), _C.stream(dev),
+    )
+    return q_row, q_col, s_row, s_col, vk_lens, vk_offs
+
+
+# ---------------------------------------------------------------------------
+# MXFP8  (quantization.cpp:736-967, dequantization_mxfp8.cu)
+# ---------------------------------------------------------------------------
+def _check_recipe(r: Optional[ScalingRecipe]):
+    if r is None:
+        return ScalingRecipe()
+    if r.use_sr or r.use_rht or r.shuffle_scale or r.shuffle_out:
+        raise NotImplementedError("MXFP8 shuffle / stochastic-rounding / RHT layouts are not implemented")
+    return r
+
+
+def quantize_mxfp8_impl(
+    x: torch.Tensor,
+    out_dtype: torch.dtype,
+    axis: Optional[int],
+    block_size: int,
+    with_trans: bool = False,
+    scaling_recipe: Optional[ScalingRecipe] = None,
+    scaling_recipe_for_trans: Optional[ScalingRecipe] = None,
+):
+    _check_hp(x)
+    assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
+    assert x.dtype in (torch.bfloat16, torch.float16), "Input must be BFloat16 or Half"
+    x = x.contiguous()
+    rr = _check_recipe(scaling_recipe)
+    rc = _check_recipe(scaling_recipe_for_trans) if with_trans else rr
+    if x.dim() == 2:
+        G, M, N = 1, x.shape[0], x.shape[1]
+    elif x.dim() == 3:
+        G, M, N = x.shape
+    else:
+        raise ValueError(f"The input tensor must be 2D or 3D but got {x.dim()}D.")
+    assert N % MXFP8_BLOCK_SIZE == 0, f"N must be divisible by {MXFP8_BLOCK_SIZE}"
+    if with_trans:
+        assert axis is None, "The axis must be None when with_trans is True."
+        row, col = True, True
+    else:
+        if x.dim() == 2:
+            assert axis in (0, 1), "The axis must be 0 or 1 when with_trans is False and x is 2D."
+            row = axis == 1
+        else:
+            assert axis in (1, 2), "The axis must be 1 or 2 when with_trans is False and x is 3D."
+            row = axis == 2
+        col = not row
+    Mp, Np = ceil_div(M, MXFP8_PADDING_ALIGN_SIZE) * 128, ceil_div(N, MXFP8_PADDING_ALIGN_SIZE) * 128
+    dev = x.device
+    q_row = e_row = q_col = e_col = None
+    if row:
+        q_row = torch.empty((G * M, Np), dtype=out_dtype, device=dev)
+        e_row = torch.empty((G * M, Np // 32), dtype=torch.uint8, device=dev)
+    if col:
+        q_col = torch.empty((G * N, Mp), dtype=out_dtype, device=dev)
+        e_col = torch.empty((G * N, Mp // 32), dtype=torch.uint8, device=dev)
+    _C.call(
+        "pta_quantize_mxfp8", _C.ptr(x), _C.in_dtype_code(x.dtype), G, M, N, _C.ptr(q_row), _C.ptr(e_row),
+        int(rr.use_2d_block), _C.ptr(q_col), _C.ptr(e_col), int(rc.use_2d_block), _C.fp8_code(out_dtype),
+        _C.stream(dev),
+    )
+
+    def shape3(t, rows):
+        return t.view(G, rows, -1) if x.dim() == 3 else t
+
+    outs = []
+    if row:
+        outs += [shape3(q_row, M), shape3(e_row, M).view(torch.float8_e8m0fnu)]
+    if col:
+        outs += [shape3(q_col, N), shape3(e_col, N).view(torch.float8_e8m0fnu)]
+    return tuple(outs)
+
+
+def dequantize_mxfp8_impl(
+    x: torch.Tensor, out_dtype: torch.dtype, axis: int, block_size: int, scale_inv: torch.Tensor
+) -> torch.Tensor:
+    """Rowwise (axis 1 / 2): y[M, N_pad]; colwise (axis 0 / 1 of 3D): y = transpose of q[N, M_pad]."""
+    assert x.is_contiguous(), "The x tensor must be contiguous."
+    assert x.dim() in (2, 3), "The x must be a 2D or 3D tensor."
+    assert scale_inv.dim() == x.dim(), "The scale_inv rank must match x."
+    assert out_dtype in (torch.float16, torch.bfloat16, torch.float32)
+    assert x.size(-1) % block_size == 0
+    if x.dim() == 2:
+        assert axis in (0, 1)
+        rowwise = axis == 1
+    else:
+        assert axis in (1, 2)
+        rowwise = axis == 2
+    e = scale_inv.contiguous().view(torch.uint8)
+    if x.dim() == 2:
+        R, C = x.shape
+        y = torch.empty((R, C) if rowwise else (C, R), dtype=out_dtype, device=x.device)
+        _C.call(
+            "pta_dequantize_mxfp8", _C.ptr(x), _C.fp8_code(x.dtype), R, C, _C.ptr(e), int(not rowwise), _C.ptr(y),
+            _C.out_dtype_code(out_dtype), _C.stream(x.device),
+        )
+        return y
+    G, R, C = x.shape
+    y = torch.empty((G, R, C) if rowwise else (G, C, R), dtype=out_dtype, device=x.device)
+    for g in range(G):
+        _C.call(
+            "pta_dequantize_mxfp8", _C.ptr(x[g]), _C.fp8_code(x.dtype), R, C, _C.ptr(e[g]), int(not rowwise),
+            _C.ptr(y[g]), _C.out_dtype_code(out_dtype), _C.stream(x.device),
+        )
+    return y
+
+
+def transpose_fp8(x: torch.Tensor) -> torch.Tensor:
+    """Byte transpose of the last two dims of a 2D / 3D fp8 tensor."""
+    x = x.contiguous()
+    if x.dim() == 2:
+        B, M, N = 1, x.shape[0], x.shape[1]
+        y = torch.empty((N, M), dtype=x.dtype, device=x.device)
+    else:
+        B, M, N = x.shape
+        y = torch.empty((B, N, M), dtype=x.dtype, device=x.device)
+    _C.call("pta_transpose_u8", _C.ptr(x), B, M, N, _C.ptr(y), _C.stream(x.device))
+    return y

@@ -1,0 +1,352 @@
+"""gemm_fp8: FP8 GEMM with autograd (drop-in for primus_turbo/pytorch/ops/gemm_fp8.py:58-743).
+
+Every forward, dgrad and wgrad GEMM runs on one gfx950 kernel in its NT form
+(both operands K-contiguous).  Where the reference transposes operands or
+scales on the host before a non-NT kernel, this build writes the transposed
+copy while quantizing (blockwise column-direction quantization and the 128x128
+weight quantization emit it directly) or byte-transposes the fp8 tensor, then
+runs NT.  The arithmetic (which bytes, which scales, fp32 accumulation per
+128-K block) is the reference's.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Union
+
+import torch
+
+from primus_turbo.pytorch.core.low_precision import (
+    Float8QuantConfig,
+    Format,
+    ScalingGranularity,
+    ScalingRecipe,
+    check_mxfp8_support,
+    float8_e4m3,
+    float8_e5m2,
+)
+from primus_turbo.pytorch.core.quantized_tensor import (
+    QuantizedTensor,
+    QuantizedTensorPair,
+    check_quantized_tensor,
+)
+from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_impl, gemm_fp8_nt
+from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+    quant_fp8_blockwise_dual_impl,
+    quant_fp8_blockwise_for_weight_impl,
+    transpose_fp8,
+)
+from primus_turbo.pytorch.ops.quantization import quantize_fp8_with_trans
+
+__all__ = ["gemm_fp8"]
+
+_BLOCK = 128
+
+
+def _get_fp8_dtype(format: Format, is_fwd_stage: bool):
+    if format == Format.E4M3:
+        return float8_e4m3
+    elif format == Format.E5M2:
+        return float8_e5m2
+    elif format == Format.HYBRID:
+        return float8_e4m3 if is_fwd_stage else float8_e5m2
+    raise ValueError(f"Unsupported FP8 format: {format}")
+
+
+def _use_nt_layout_gemm_in_bwd(trans_a: bool, trans_b: bool) -> bool:
+    # gemm_fp8.py:49-55: on gfx950 the NT forward runs every backward GEMM as NT
+    return (not trans_a) and trans_b
+
+
+def _ceil(a: int, b: int) -> int:
+    return (a + b - 1) // b
+
+
+def _pad_cols(x: torch.Tensor, mult: int) -> torch.Tensor:
+    """Zero-pad the last dim of an fp8 matrix to a multiple of ``mult`` (exact for GEMM K)."""
+    k = x.shape[-1]
+    if k % mult == 0:
+        return x.contiguous()
+    out = torch.zeros((*x.shape[:-1], _ceil(k, mult) * mult), dtype=x.dtype, device=x.device)
+    out[..., :k] = x
+    return out
+
+
+def _pad_cols16(x: torch.Tensor) -> torch.Tensor:
+    return _pad_cols(x, 16)
+
+
+def _nt_or_impl(a, sa, trans_a, b, sb, trans_b, out_dtype, trans_c, gran: ScalingGranularity):
+    """gemm_fp8_impl with zero K-padding for K not a multiple of 16 (tensorwise / rowwise)."""
+    k = a.shape[0] if trans_a else a.shape[1]
+    if k % 16 != 0:
+        # bring both operands to K-contiguous form, pad K, run NT
+        a_k = transpose_fp8(a) if trans_a else a
+        b_k = b if trans_b else transpose_fp8(b)
+        return gemm_fp8_impl(_pad_cols16(a_k), sa, False, _pad_cols16(b_k), sb, True, out_dtype, trans_c, gran.value)
+    return gemm_fp8_impl(a, sa, trans_a, b, sb, trans_b, out_dtype, trans_c, gran.value)
+
+
+# ===========================================================================
+# TENSORWISE
+# ===========================================================================
+class FP8GemmTensorFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, a_t, b_t, trans_a, trans_b, out_dtype, config):
+        g = ScalingGranularity.TENSORWISE
+        nt_bwd = _use_nt_layout_gemm_in_bwd(trans_a, trans_b)
+        if isinstance(a, QuantizedTensor):
+            qa = a
+            check_quantized_tensor(qa, config)
+        else:
+            qa = QuantizedTensor.quantize(a, _get_fp8_dtype(config.format, True), g, axis=-1)
+        if isinstance(b, QuantizedTensor):
+            qb = b
+            check_quantized_tensor(qb, config)
+        else:
+            qb = QuantizedTensor.quantize(b, _get_fp8_dtype(config.format, True), g, axis=-1)
+        out = _nt_or_impl(qa.qdata, qa.scale_inv, trans_a, qb.qdata, qb.scale_inv, trans_b, out_dtype, False, g)
+        if nt_bwd:
+            qa_t = a_t if isinstance(a_t, QuantizedTensor) else qa.t()
+            qb_t = b_t if isinstance(b_t, QuantizedTensor) else qb.t()
+            ctx.save_for_backward(qa_t.qdata, qa_t.scale_inv, qb_t.qdata, qb_t.scale_inv)
+        else:
+            ctx.save_for_backward(qa.qdata, qa.scale_inv, qb.qdata, qb.scale_inv)
+        ctx.trans_a, ctx.trans_b, ctx.out_dtype, ctx.config, ctx.nt_bwd = trans_a, trans_b, out_dtype, config, nt_bwd
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        g = ScalingGranularity.TENSORWISE
+        grad_out = grad_out.contiguous()
+        x0, s0, x1, s1 = ctx.saved_tensors
+        qg = QuantizedTensor.quantize(grad_out, _get_fp8_dtype(ctx.config.format, False), g, axis=-1)
+        if ctx.nt_bwd:
+            a_t, a_t_s, b_t, b_t_s = x0, s0, x1, s1
+            a_grad = _nt_or_impl(qg.qdata, qg.scale_inv, False, b_t, b_t_s, True, ctx.out_dtype, False, g)
+            g_t = transpose_fp8(qg.qdata)
+            b_grad = _nt_or_impl(a_t, a_t_s, False, g_t, qg.scale_inv, True, ctx.out_dtype, ctx.trans_b, g)
+        else:
+            a8, sa, b8, sb = x0, s0, x1, s1
+            a_grad = _nt_or_impl(qg.qdata, qg.scale_inv, False, b8, sb, not ctx.trans_b, ctx.out_dtype, ctx.trans_a, g)
+            b_grad = _nt_or_impl(a8, sa, not ctx.trans_a, qg.qdata, qg.scale_inv, False, ctx.out_dtype, ctx.trans_b, g)
+        return a_grad, b_grad, None, None, None, None, None, None
+
+
+# ===========================================================================
+# ROWWISE (gemm_fp8.py:231-379): the backward copies are re-quantized along
+# the other axis from the dequantized forward tensors, as in the reference.
+# ===========================================================================
+class FP8GemmRowFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, a_t, b_t, trans_a, trans_b, out_dtype, config):
+        assert trans_a == False, "trans_a has to be False"
+        g = ScalingGranularity.ROWWISE
+        if isinstance(a, QuantizedTensor):
+            qa = a
+            check_quantized_tensor(qa, config, axis=-1)
+        else:
+            qa = QuantizedTensor.quantize(a, _get_fp8_dtype(config.format, True), g, axis=-1,
+                                          block_size=config.block_size)
+        if a_t is None:
+            qa_t = QuantizedTensor.quantize(qa.dequantize(), qa.real_dtype, g, axis=-2, block_size=config.block_size)
+        else:
+            qa_t = a_t
+        b_axis = -1 if trans_b else -2
+        if isinstance(b, QuantizedTensor):
+            check_quantized_tensor(b, config, axis=b_axis)
+            qb = b
+        else:
+            qb = QuantizedTensor.quantize(b, _get_fp8_dtype(config.format, True), g, axis=b_axis,
+                                          block_size=config.block_size)
+        if b_t is None:
+            qb_t = QuantizedTensor.quantize(qb.dequantize(), qb.real_dtype, g, axis=-2 if trans_b else -1,
+                                            block_size=config.block_size)
+        else:
+            qb_t = b_t
+        out = _nt_or_impl(qa.qdata, qa.scale_inv, trans_a, qb.qdata, qb.scale_inv, trans_b, out_dtype, False, g)
+        ctx.save_for_backward(qa_t.qdata, qa_t.scale_inv, qb_t.qdata, qb_t.scale_inv)
+        ctx.trans_a, ctx.trans_b, ctx.out_dtype, ctx.config = trans_a, trans_b, out_dtype, config
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        g = ScalingGranularity.ROWWISE
+        grad_out = grad_out.contiguous()
+        a_t, a_t_s, b_t, b_t_s = ctx.saved_tensors
+        gd = _get_fp8_dtype(ctx.config.format, False)
+        qg = QuantizedTensor.quantize(grad_out, gd, g, axis=-1, block_size=ctx.config.block_size)
+        a_grad = _nt_or_impl(qg.qdata, qg.scale_inv, False, b_t, b_t_s, not ctx.trans_b, ctx.out_dtype, ctx.trans_a, g)
+        qg_t = QuantizedTensor.quantize(grad_out, gd, g, axis=-2, block_size=ctx.config.block_size)
+        b_grad = _nt_or_impl(a_t, a_t_s, not ctx.trans_a, qg_t.qdata, qg_t.scale_inv, False, ctx.out_dtype,
+                             ctx.trans_b, g)
+        return a_grad, b_grad, None, None, None, None, None, None
+
+
+# ===========================================================================
+# BLOCKWISE (gemm_fp8.py:382-506): activations 1 x 128, weights 128 x 128.
+# ===========================================================================
+def _weight_nk_kn(qw: torch.Tensor, trans_b: bool):
+    """(weight as [N, K] rows, weight as [K, N] rows) from its stored layout."""
+    qw_t = transpose_fp8(qw)
+    return (qw, qw_t) if trans_b else (qw_t, qw)
+
+
+class FP8GemmBlockFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, a_t, b_t, trans_a, trans_b, out_dtype, config):
+        assert trans_a == False, "trans_a has to be False"
+        assert config.block_size == _BLOCK, "BLOCKWISE supports block_size 128"
+        gran = ScalingGranularity.BLOCKWISE
+        fdt = _get_fp8_dtype(config.format, True)
+        M, K = a.shape
+        # --- A: row scales [M, K/128] (fwd) + column copy transposed [K, M_pad] (wgrad)
+        if isinstance(a, QuantizedTensor):
+            check_quantized_tensor(a, config, axis=-1)
+            a_row, a_row_s = a.qdata, a.scale_inv
+            if a_t is None:
+                a_t = QuantizedTensor.quantize(a.dequantize(), fdt, gran, axis=-2, block_size=config.block_size)
+            a_colT = _pad_cols(transpose_fp8(a_t.qdata), _BLOCK)
+            a_col_s = a_t.scale_inv
+        else:
+            a_row, a_row_s, a_colT, a_col_s = quant_fp8_blockwise_dual_impl(
+                a.detach().contiguous(), fdt, block_size=config.block_size, col_transposed=True
+            )
+        # --- B: 128 x 128 blocks, reused by fwd and dgrad
+        recipe = ScalingRecipe(use_2d_block=True)
+        if isinstance(b, QuantizedTensor):
+            check_quantized_tensor(b, config, scaling_recipe=recipe)
+            w_nk, w_kn = _weight_nk_kn(b.qdata, trans_b)
+            w_s = b.scale_inv
+        else:
+            qw, w_s, qw_t = quant_fp8_blockwise_for_weight_impl(
+                b.detach().contiguous(), fdt, block_size=config.block_size, with_transpose=True
+            )
+            w_nk, w_kn = (qw, qw_t) if trans_b else (qw_t, qw)
+        N = w_nk.shape[0]
+        a_row = _pad_cols16(a_row)
+        w_nk = _pad_cols16(w_nk)
+        # weight scale element (n-block, k-block): [N/128, K/128] if trans_b else [K/128, N/128]
+        nbk = _ceil(K, _BLOCK)
+        nbn = _ceil(N, _BLOCK)
+        w_str_nk = (nbk, 1) if trans_b else (1, nbn)  # rows n, blocks k
+        w_str_kn = (1, nbk) if trans_b else (nbn, 1)  # rows k, blocks n
+        out = gemm_fp8_nt(a_row, w_nk, out_dtype, gran, a_row_s, (nbk, 1), False, w_s, w_str_nk, True)
+        ctx.save_for_backward(a_colT, a_col_s, _pad_cols(w_kn, _BLOCK), w_s)
+        ctx.w_str_kn = w_str_kn
+        ctx.trans_b, ctx.out_dtype, ctx.config = trans_b, out_dtype, config
+        ctx.M, ctx.N, ctx.K = M, N, K
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        gran = ScalingGranularity.BLOCKWISE
+        a_colT, a_col_s, w_kn, w_s = ctx.saved_tensors
+        M, N, K = ctx.M, ctx.N, ctx.K
+        gdt = _get_fp8_dtype(ctx.config.format, False)
+        g_row, g_row_s, g_colT, g_col_s = quant_fp8_blockwise_dual_impl(
+            grad_out.contiguous(), gdt, block_size=ctx.config.block_size, col_transposed=True
+        )
+        nbn = _ceil(N, _BLOCK)
+        # dgrad: dA[M, K] = g_row[M, N] . w_kn[K, N]^T
+        grad_a = gemm_fp8_nt(_pad_cols16(g_row), w_kn, ctx.out_dtype, gran, g_row_s, (nbn, 1), False,
+                             w_s, ctx.w_str_kn, True)
+        # wgrad over M (column-direction copies, transposed, M padded to 128)
+        if ctx.trans_b:  # dW[N, K] = g_colT[N, M] . a_colT[K, M]^T
+            grad_b = gemm_fp8_nt(g_colT, a_colT, ctx.out_dtype, gran, g_col_s, (1, N), False, a_col_s, (1, K), False)
+        else:  # dW[K, N]
+            grad_b = gemm_fp8_nt(a_colT, g_colT, ctx.out_dtype, gran, a_col_s, (1, K), False, g_col_s, (1, N), False)
+        return grad_a, grad_b, None, None, None, None, None, None
+
+
+# ===========================================================================
+# MX_BLOCKWISE (gemm_fp8.py:509-647): NT only, E8M0 per 32-K block.
+# ===========================================================================
+def _mx_gemm(a_q, a_e, b_q, b_e, out_dtype):
+    K = a_q.shape[1]
+    assert b_q.shape[1] == K
+    return gemm_fp8_nt(a_q, b_q, out_dtype, ScalingGranularity.MX_BLOCKWISE, a_e, (K // 32, 0), False,
+                       b_e, (K // 32, 0), False)
+
+
+class FP8GemmMXFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, a_t, b_t, trans_a, trans_b, out_dtype, config):
+        ok, reason = check_mxfp8_support()
+        assert ok, reason
+        assert trans_a == False and trans_b == True, "trans_a has to be False and trans_b has to be True"
+        fdt = _get_fp8_dtype(config.format, True)
+        gran, bs = config.granularity, config.block_size
+        ra = ScalingRecipe()
+        if isinstance(a, QuantizedTensor):
+            check_quantized_tensor(a, config, axis=-1, scaling_recipe=ra)
+            a_row, a_row_s = a.qdata, a.scale_inv
+            if a_t is None:
+                a_t = QuantizedTensor.quantize(a.dequantize(), a.real_dtype, gran, axis=-2, block_size=bs,
+                                               scaling_recipe=ra)
+            a_col, a_col_s = a_t.qdata, a_t.scale_inv
+        else:
+            a_row, a_row_s, a_col, a_col_s = quantize_fp8_with_trans(a.detach(), fdt, gran, block_size=bs,
+                                                                     scaling_recipe=ra)
+        rb = ScalingRecipe(use_2d_block=True)
+        if isinstance(b, QuantizedTensor):
+            check_quantized_tensor(b, config, axis=-1, scaling_recipe=rb)
+            b_row, b_row_s = b.qdata, b.scale_inv
+            if b_t is None:
+                b_t = QuantizedTensor.quantize(b.dequantize(), b.real_dtype, gran, axis=-2, block_size=bs,
+                                               scaling_recipe=rb)
+            b_col, b_col_s = b_t.qdata, b_t.scale_inv
+        else:
+            b_row, b_row_s, b_col, b_col_s = quantize_fp8_with_trans(
+                b.detach(), fdt, gran, block_size=bs, scaling_recipe=rb, scaling_recipe_for_trans=rb
+            )
+        out = _mx_gemm(a_row, a_row_s, b_row, b_row_s, out_dtype)
+        ctx.save_for_backward(a_col, a_col_s, b_col, b_col_s)
+        ctx.out_dtype, ctx.config = out_dtype, config
+        ctx.M, ctx.N, ctx.K = a.shape[0], b.shape[0], a.shape[1]
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        a_col, a_col_s, b_col, b_col_s = ctx.saved_tensors
+        gdt = _get_fp8_dtype(ctx.config.format, False)
+        grad_out = grad_out.reshape(grad_out.shape[0], -1).contiguous()
+        g_row, g_row_s, g_col, g_col_s = quantize_fp8_with_trans(
+            grad_out, gdt, ctx.config.granularity, block_size=ctx.config.block_size
+        )
+        grad_a = _mx_gemm(g_row, g_row_s, b_col, b_col_s, ctx.out_dtype)  # [M, K]
+        grad_b = _mx_gemm(g_col, g_col_s, a_col, a_col_s, ctx.out_dtype)  # [N, K]
+        return grad_a[: ctx.M, : ctx.K], grad_b[: ctx.N, : ctx.K], None, None, None, None, None, None
+
+
+@torch._dynamo.disable(recursive=True)
+def gemm_fp8(
+    a: Union[torch.Tensor, QuantizedTensor, QuantizedTensorPair],
+    b: Union[torch.Tensor, QuantizedTensor, QuantizedTensorPair],
+    trans_a: bool = False,
+    trans_b: bool = False,
+    out_dtype: Optional[torch.dtype] = None,
+    config: Optional[Float8QuantConfig] = None,
+) -> torch.Tensor:
+    """C = op(a) @ op(b) with FP8 quantization in forward and backward.
+
+    a: [M, K] (or [K, M] with trans_a); b: [K, N] (or [N, K] with trans_b).
+    config defaults to TENSORWISE E4M3; out_dtype defaults to promote_types(a, b).
+    """
+    if config is None:
+        config = Float8QuantConfig()
+    a_data, a_data_t = (a.data, a.data_t) if isinstance(a, QuantizedTensorPair) else (a, None)
+    b_data, b_data_t = (b.data, b.data_t) if isinstance(b, QuantizedTensorPair) else (b, None)
+    assert a_data.ndim == 2, "Only 2D tensors are supported"
+    assert b_data.ndim == 2, "Only 2D tensors are supported"
+    if out_dtype is None:
+        out_dtype = torch.promote_types(a_data.dtype, b_data.dtype)
+    args = (a_data, b_data, a_data_t, b_data_t, trans_a, trans_b, out_dtype, config)
+    if config.granularity == ScalingGranularity.TENSORWISE:
+        return FP8GemmTensorFunction.apply(*args)
+    elif config.granularity == ScalingGranularity.ROWWISE:
+        return FP8GemmRowFunction.apply(*args)
+    elif config.granularity == ScalingGranularity.BLOCKWISE:
+        return FP8GemmBlockFunction.apply(*args)
+    elif config.granularity == ScalingGranularity.MX_BLOCKWISE:
+        return FP8GemmMXFunction.apply(*args)
+    raise ValueError(f"Unsupported FP8 ScalingGranularity: {config.granularity}")

@@ -1,0 +1,66 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+that include/primus_turbo_amd.h declares, the Python binding table matches the
+header, and argument validation fails before any device work."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "primus_turbo_amd.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(pta_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "pta_gemm_fp8" in names and "pta_quantize_fp8_blockwise_dual" in names
+    assert len(names) >= 25
+
+
+def test_library_exports_every_declared_symbol():
+    from primus_turbo.pytorch import _C
+
+    lib = ctypes.CDLL(_C.lib_path())
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_table_matches_header():
+    from primus_turbo.pytorch import _C
+
+    assert sorted(_C.SIGNATURES) == _declared()
+
+
+def test_argument_errors_raise_without_gpu():
+    from primus_turbo.pytorch import _C
+
+    lib = _C.load()
+    assert lib.pta_abi_version() == 1
+    # NULL input: rejected on the host before any HIP call
+    rc = lib.pta_quantize_fp8_blockwise(None, 2, 128, 128, 128, 1, None, None, 0, None)
+    assert rc == -1
+    assert b"NULL" in lib.pta_last_error()
+    # unsupported block size
+    rc = lib.pta_quantize_fp8_blockwise(ctypes.c_void_p(16), 2, 128, 128, 64, 1, None, None, 0, None)
+    assert rc == -1 and b"block size" in lib.pta_last_error()
+    # bad granularity for the GEMM
+    rc = lib.pta_gemm_fp8(None, 0, None, 0, None, 0, None, 1, None, 2, 0, 1, 1, 16, 9, None, 0, None)
+    assert rc == -1 and b"granularity" in lib.pta_last_error()
+    with pytest.raises(RuntimeError, match="granularity"):
+        _C.call("pta_gemm_fp8", None, 0, None, 0, None, 0, None, 1, None, 2, 0, 1, 1, 16, 9, None, 0, None)
+
+
+def test_workspace_queries():
+    from primus_turbo.pytorch import _C
+
+    assert _C.query("pta_gemm_fp8_workspace_size", 128, 256, 512, 0, 1, 3) == 0
+    assert _C.query("pta_gemm_fp8_workspace_size", 128, 256, 512, 1, 0, 3) >= 128 * 512 + 256 * 512
+    assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 4, 100, 1) == 0
+    assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 1, 100, 64) > 0

@@ -1,0 +1,146 @@
+"""GPU parity of the grouped FP8 GEMMs: per-group results against the fp64
+oracle, empty groups, zeroed output tail and the variable-K wgrad."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import f32, randn, u8
+
+pytestmark = pytest.mark.gpu
+
+SNR_MIN = 40.0
+REL_MAX = 1e-2
+
+
+def _mods():
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import Float8QuantConfig, Format, ScalingGranularity, ScalingRecipe
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_fp8_impl import (
+        grouped_gemm_fp8_impl,
+        grouped_gemm_fp8_variable_k_impl,
+    )
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_segment_m_row_col_impl,
+    )
+
+    return (turbo, Float8QuantConfig, Format, ScalingGranularity, ScalingRecipe, grouped_gemm_fp8_impl,
+            grouped_gemm_fp8_variable_k_impl, group_offs_from_lens, quant_fp8_blockwise_segment_m_row_col_impl)
+
+
+def _check(out, ref, what):
+    o = np.asarray(out, np.float64)
+    snr = O.snr_db(ref, o)
+    rel = O.max_rel_err(ref, o)
+    assert snr >= SNR_MIN and rel <= REL_MAX, f"{what}: SNR {snr:.1f} dB, rel {rel:.2e}"
+
+
+LENS = [[300, 0, 513, 128, 59], [0, 0, 256], [1000], [64, 64, 64, 64]]
+
+
+@pytest.mark.parametrize("lens", LENS)
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_grouped_blockwise_fwd_vs_oracle(lens, trans_b):
+    (turbo, _, _, SG, SR, gg, _, offs_from, segq) = _mods()
+    G, K, N = len(lens), 512, 384
+    M = sum(lens)
+    a = randn((M, K), seed=1).cuda()
+    w = randn((G, N, K) if trans_b else (G, K, N), seed=2, scale=0.02).cuda()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = offs_from(gl)
+    qdt = torch.float8_e4m3fn
+    a_row, _, s_row_t, _, _, _ = segq(a, qdt, 128, gl, go)
+    qw, sw = turbo.ops.quantize_fp8(w, qdt, SG.BLOCKWISE, block_size=128, scaling_recipe=SR(use_2d_block=True))
+    out = gg(a_row, qw, s_row_t, sw, gl, go, False, trans_b, torch.bfloat16, SG.BLOCKWISE.value)
+    da = O.dequant_block1d(u8(a_row), 0, f32(s_row_t).T, 1)
+    dw = O.dequant_block2d(u8(qw), 0, f32(sw))
+    o = f32(out)
+    off = 0
+    for g, L in enumerate(lens):
+        if L:
+            ref = O.gemm_ref(da[off:off + L], dw[g], False, trans_b)
+            _check(o[off:off + L], ref, f"group {g}")
+        off += L
+
+
+@pytest.mark.parametrize("lens", LENS)
+def test_grouped_tail_is_zero(lens):
+    (turbo, _, _, SG, SR, gg, _, offs_from, segq) = _mods()
+    G, K, N = len(lens), 256, 256
+    M = sum(lens)
+    Mtot = M + 77  # over-allocated rows past the last group
+    a = randn((Mtot, K), seed=3).cuda()
+    w = randn((G, N, K), seed=4).cuda()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = offs_from(gl)
+    qa, sa = turbo.ops.quantize_fp8(a, torch.float8_e4m3fn, SG.TENSORWISE)
+    qw, sw = turbo.ops.quantize_fp8(w, torch.float8_e4m3fn, SG.TENSORWISE)
+    out = gg(qa, qw, sa, sw, gl, go, False, True, torch.bfloat16, SG.TENSORWISE.value)
+    assert torch.all(out[M:] == 0)
+    da = O.dequant_tensorwise(u8(qa), 0, f32(sa))
+    dw = O.dequant_tensorwise(u8(qw), 0, f32(sw))
+    off = 0
+    for g, L in enumerate(lens):
+        if L:
+            _check(f32(out)[off:off + L], O.gemm_ref(da[off:off + L], dw[g], False, True), f"group {g}")
+        off += L
+
+
+@pytest.mark.parametrize("lens", LENS)
+@pytest.mark.parametrize("trans_c", [True, False])
+def test_grouped_variable_k_blockwise_vs_oracle(lens, trans_c):
+    (turbo, _, _, SG, _, _, gvk, offs_from, segq) = _mods()
+    G, K, N = len(lens), 384, 256
+    M = sum(lens)
+    a = randn((max(M, 1), K), seed=5).cuda()[:M].contiguous()
+    gout = randn((max(M, 1), N), seed=6).cuda()[:M].contiguous()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = offs_from(gl)
+    qdt = torch.float8_e4m3fn
+    _, a_col, _, a_s_col, vl, vo = segq(a, qdt, 128, gl, go)
+    _, g_col, _, g_s_col, _, _ = segq(gout, qdt, 128, gl, go)
+    out = gvk(a_col, g_col, a_s_col, g_s_col, vl, vo, True, False, trans_c, torch.bfloat16, SG.BLOCKWISE.value)
+    P = int(vo[-1])
+    da = O.dequant_block1d(u8(a_col)[:P], 0, f32(a_s_col)[: P // 128], 0)
+    dg = O.dequant_block1d(u8(g_col)[:P], 0, f32(g_s_col)[: P // 128], 0)
+    vo_h = vo.cpu().numpy()
+    o = f32(out)
+    for g in range(G):
+        s, e = vo_h[g], vo_h[g + 1]
+        if e == s:
+            assert not o[g].any(), "empty group must give a zero slice"
+            continue
+        ref = O.gemm_ref(da[s:e], dg[s:e], True, False, trans_c)
+        _check(o[g], ref, f"group {g}")
+
+
+@pytest.mark.parametrize("lens", [[300, 0, 513, 128, 59], [64, 64, 64, 64]])
+@pytest.mark.parametrize("gran", ["BLOCKWISE", "TENSORWISE", "ROWWISE"])
+def test_grouped_gemm_fp8_autograd(lens, gran):
+    """The reference's grouped criterion: SNR vs a per-group fp32 matmul
+    (tests/pytorch/ops/test_grouped_gemm_fp8.py:163-175)."""
+    (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
+    g = getattr(SG, gran)
+    cfg = Cfg(granularity=g, format=Format.E4M3, block_size=128 if gran == "BLOCKWISE" else None)
+    G, K, N = len(lens), 512, 256
+    M = sum(lens)
+    gen = torch.Generator().manual_seed(0)
+    a = torch.randn((M, K), generator=gen).bfloat16().cuda().requires_grad_()
+    w = torch.randn((G, N, K), generator=gen).bfloat16().cuda().requires_grad_()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    out = turbo.ops.grouped_gemm_fp8(a, w, gl, trans_b=True, config=cfg)
+    grad = torch.randn((M, N), generator=gen).bfloat16().cuda()
+    out.backward(grad)
+    a_ref = a.detach().float().requires_grad_()
+    w_ref = w.detach().float().requires_grad_()
+    outs, off = [], 0
+    for i, L in enumerate(lens):
+        outs.append(a_ref[off:off + L] @ w_ref[i].T)
+        off += L
+    ref = torch.cat(outs)
+    ref.backward(grad.float())
+    for name, x, r in (("out", out, ref), ("dA", a.grad, a_ref.grad), ("dW", w.grad, w_ref.grad)):
+        s = O.snr_db(f32(r), f32(x))
+        assert s > 25, f"{name} SNR {s:.1f} dB"

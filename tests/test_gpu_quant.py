@@ -1,0 +1,313 @@
+"""GPU parity of the quantization kernels: FP8 bytes and scales must be
+bit-identical to (a) the CPU oracle and (b) where the reference's own HIP
+kernels build (oracle/_ref), to the reference's kernels run on the same GPU."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import (
+    FMT,
+    assert_bytes_equal,
+    assert_f32_bitexact,
+    f32,
+    randn,
+    ref_lib,
+    stream,
+    u8,
+)
+
+pytestmark = pytest.mark.gpu
+
+FP8 = [torch.float8_e4m3fn, torch.float8_e5m2]
+
+
+def _turbo():
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity, ScalingRecipe
+
+    return turbo, ScalingGranularity, ScalingRecipe
+
+
+def _input(shape, dtype=torch.bfloat16, seed=0, special=True):
+    x = randn(shape, dtype=dtype, seed=seed, outliers=0.001)
+    if special and x.numel() >= 8:
+        flat = x.view(-1)
+        flat[0] = 0.0
+        flat[1] = -0.0
+        flat[2] = 1e-6
+        flat[3] = -3.0e2
+    return x
+
+
+# ---------------------------------------------------------------------------
+# tensorwise
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(512, 1024), (1000, 37), (3, 5, 7), (4096, 1536)])
+@pytest.mark.parametrize("qdt", FP8)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_tensorwise_vs_oracle(shape, qdt, dtype):
+    turbo, SG, _ = _turbo()
+    x = _input(shape, dtype)
+    q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.TENSORWISE)
+    qo, so = O.quant_tensorwise(x, FMT[qdt])
+    assert q.shape == x.shape and s.shape == () and q.dtype == qdt
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+    assert_f32_bitexact(f32(s), so, "scale_inv")
+
+
+@pytest.mark.parametrize("qdt", FP8)
+def test_tensorwise_every_bf16_value(qdt):
+    """All finite bf16 values within +-max with amax == max (scale exactly 1):
+    the bytes are the RNE encodings of the inputs themselves."""
+    turbo, SG, _ = _turbo()
+    u = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    mx = O.FP8_MAX[FMT[qdt]]
+    vals = u[np.isfinite(u) & (np.abs(u) <= mx)]
+    vals = np.concatenate([vals, [mx]]).astype(np.float32)
+    x = torch.from_numpy(vals).to(torch.bfloat16)
+    q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.TENSORWISE)
+    assert float(s) == 1.0
+    exp = np.array([O.fp8_encode_scalar(float(v), FMT[qdt]) for v in vals], dtype=np.uint8)
+    assert_bytes_equal(u8(q), exp, "rne bytes")
+
+
+@pytest.mark.parametrize("n", [1, 4096, 1 << 20, (1 << 20) + 13])
+@pytest.mark.parametrize("qdt", FP8)
+def test_tensorwise_vs_reference_kernels(n, qdt):
+    L = ref_lib()
+    if L is None:
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    turbo, SG, _ = _turbo()
+    x = _input((n,), seed=3).cuda()
+    q, s = turbo.ops.quantize_fp8(x, qdt, SG.TENSORWISE)
+    qr = torch.empty_like(q)
+    sr = torch.empty((), dtype=torch.float32, device="cuda")
+    ws = torch.empty(L.ref_tensorwise_ws_bytes(n), dtype=torch.uint8, device="cuda")
+    assert L.ref_quant_tensorwise(x.data_ptr(), n, FMT[qdt], qr.data_ptr(), sr.data_ptr(), ws.data_ptr(), stream()) == 0
+    torch.cuda.synchronize()
+    assert_bytes_equal(u8(q), u8(qr), "fp8 bytes vs reference kernel")
+    assert_f32_bitexact(f32(s), f32(sr), "scale_inv vs reference kernel")
+
+
+# ---------------------------------------------------------------------------
+# rowwise
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize(
+    "shape,axis",
+    [((256, 4096), -1), ((33, 100), -1), ((7, 5000), 1), ((3, 20000), -1), ((300, 96), 0), ((4, 300, 96), 1),
+     ((2, 3, 64), 0)],
+)
+@pytest.mark.parametrize("qdt", FP8)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rowwise_vs_oracle(shape, axis, qdt, dtype):
+    turbo, SG, _ = _turbo()
+    x = _input(shape, dtype, seed=1)
+    q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.ROWWISE, axis=axis)
+    qo, so = O.quant_rowwise(x, FMT[qdt], axis)
+    assert tuple(s.shape) == so.shape
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+    assert_f32_bitexact(f32(s), so, "scale_inv")
+
+
+@pytest.mark.parametrize("shape,axis", [((256, 4096), -1), ((33, 100), -1), ((300, 96), 0), ((4, 300, 96), 1)])
+@pytest.mark.parametrize("qdt", FP8)
+def test_rowwise_vs_reference_kernels(shape, axis, qdt):
+    L = ref_lib()
+    if L is None:
+        pytest.skip("oracle/_ref not built")
+    turbo, SG, _ = _turbo()
+    x = _input(shape, seed=2).cuda()
+    q, s = turbo.ops.quantize_fp8(x, qdt, SG.ROWWISE, axis=axis)
+    qr = torch.empty_like(q)
+    ax = axis % x.dim()
+    B = int(np.prod(shape[:ax])) if ax > 0 else 1
+    M = shape[ax]
+    N = int(np.prod(shape[ax + 1:])) if ax + 1 < len(shape) else 1
+    sc = torch.empty(B * N, dtype=torch.float32, device="cuda")
+    sr = torch.empty(B * N, dtype=torch.float32, device="cuda")
+    if N == 1:
+        assert L.ref_quant_rowwise_last(x.data_ptr(), B, M, FMT[qdt], qr.data_ptr(), sc.data_ptr(), sr.data_ptr(),
+                                        stream()) == 0
+    else:
+        ws = torch.empty(L.ref_rowwise_col_ws_bytes(B, M, N), dtype=torch.uint8, device="cuda")
+        assert L.ref_quant_rowwise_col(x.data_ptr(), B, M, N, FMT[qdt], qr.data_ptr(), sc.data_ptr(), sr.data_ptr(),
+                                       ws.data_ptr(), stream()) == 0
+    torch.cuda.synchronize()
+    assert_bytes_equal(u8(q), u8(qr), "fp8 bytes vs reference kernel")
+    assert_f32_bitexact(f32(s).reshape(-1), f32(sr), "scale_inv vs reference kernel")
+
+
+# ---------------------------------------------------------------------------
+# blockwise
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(256, 512), (300, 200), (128, 128), (1, 1000), (640, 7168)])
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("qdt", FP8)
+def test_blockwise_1d_vs_oracle(shape, axis, qdt):
+    turbo, SG, _ = _turbo()
+    x = _input(shape, seed=4)
+    q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.BLOCKWISE, block_size=128, axis=axis)
+    qo, so = O.quant_block1d(x, FMT[qdt], axis)
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+    assert_f32_bitexact(f32(s), so, "scales")
+
+
+@pytest.mark.parametrize("shape", [(256, 512), (300, 200), (4096, 2048)])
+@pytest.mark.parametrize("qdt", FP8)
+def test_blockwise_dual_vs_oracle(shape, qdt):
+    turbo, SG, _ = _turbo()
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import quant_fp8_blockwise_dual_impl
+
+    x = _input(shape, seed=5)
+    qr, sr, qc, sc = turbo.ops.quantize_fp8_with_trans(x.cuda(), qdt, SG.BLOCKWISE, block_size=128)
+    o = O.quant_block_dual(x, FMT[qdt])
+    assert_bytes_equal(u8(qr), o[0], "row bytes")
+    assert_f32_bitexact(f32(sr), o[1], "row scales")
+    assert_bytes_equal(u8(qc), o[2], "col bytes")
+    assert_f32_bitexact(f32(sc), o[3], "col scales")
+    # transposed column output: same bytes, [N, roundup(M,128)] with zero padding
+    _, _, qct, sct = quant_fp8_blockwise_dual_impl(x.cuda(), qdt, 128, col_transposed=True)
+    M, N = shape
+    qct = u8(qct)
+    assert_bytes_equal(qct[:, :M], o[2].T, "transposed col bytes")
+    assert not qct[:, M:].any(), "padding must be zero"
+    assert_f32_bitexact(f32(sct), o[3], "col scales (transposed path)")
+
+
+@pytest.mark.parametrize("shape", [(512, 384), (300, 260), (2, 300, 260), (4, 256, 640)])
+@pytest.mark.parametrize("qdt", FP8)
+def test_blockwise_weight_vs_oracle_and_reference(shape, qdt):
+    turbo, SG, SR = _turbo()
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import quant_fp8_blockwise_for_weight_impl
+
+    w = _input(shape, seed=6)
+    q, s = turbo.ops.quantize_fp8(w.cuda(), qdt, SG.BLOCKWISE, block_size=128, scaling_recipe=SR(use_2d_block=True))
+    qo, so = O.quant_block_weight(w, FMT[qdt])
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+    assert_f32_bitexact(f32(s), so, "scales")
+    _, _, qt = quant_fp8_blockwise_for_weight_impl(w.cuda(), qdt, 128, with_transpose=True)
+    M = shape[-2]
+    qt = u8(qt)
+    assert_bytes_equal(qt[..., :M], np.swapaxes(qo, -1, -2), "transposed copy")
+    assert not qt[..., M:].any()
+    L = ref_lib()
+    if L is not None:
+        wc = w.cuda().contiguous()
+        B = shape[0] if len(shape) == 3 else 1
+        qr = torch.empty_like(q)
+        sr = torch.empty_like(s)
+        assert L.ref_quant_weight(wc.data_ptr(), B, shape[-2], shape[-1], FMT[qdt], qr.data_ptr(), sr.data_ptr(),
+                                  stream()) == 0
+        torch.cuda.synchronize()
+        assert_bytes_equal(u8(q), u8(qr), "fp8 bytes vs reference kernel")
+        assert_f32_bitexact(f32(s), f32(sr), "scales vs reference kernel")
+
+
+@pytest.mark.parametrize("lens", [[100, 0, 300, 128, 5], [0, 0, 64], [1000], [256, 256, 0, 0]])
+@pytest.mark.parametrize("qdt", FP8)
+def test_segment_vs_oracle_and_reference(lens, qdt):
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import quant_fp8_blockwise_segment_m_row_col_impl
+
+    M, N = sum(lens), 384
+    x = _input((max(M, 1), N), seed=7)[:M].contiguous()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = group_offs_from_lens(gl)
+    qr, qc, sr, sc, vl, vo = quant_fp8_blockwise_segment_m_row_col_impl(x.cuda(), qdt, 128, gl, go)
+    o = O.quant_block_segment(x, FMT[qdt], lens)
+    np.testing.assert_array_equal(vl.cpu().numpy(), o[4])
+    np.testing.assert_array_equal(vo.cpu().numpy(), o[5])
+    P = int(o[5][-1])
+    assert_bytes_equal(u8(qr), o[0], "row bytes")
+    assert_f32_bitexact(f32(sr), o[2], "row scales (transposed)")
+    assert_bytes_equal(u8(qc)[:P], o[1][:P], "padded col bytes")
+    assert_f32_bitexact(f32(sc)[: P // 128], o[3][: P // 128], "col scales")
+    L = ref_lib()
+    if L is not None and M > 0:
+        xc = x.cuda().contiguous()
+        G = len(lens)
+        qr2, qc2 = torch.empty_like(qr), torch.zeros_like(qc)
+        sr2, sc2 = torch.empty_like(sr), torch.zeros_like(sc)
+        vl2, vo2 = torch.empty_like(vl), torch.empty_like(vo)
+        assert L.ref_quant_segment(xc.data_ptr(), M, N, G, gl.data_ptr(), go.data_ptr(), FMT[qdt], qr2.data_ptr(),
+                                   qc2.data_ptr(), sr2.data_ptr(), sc2.data_ptr(), vl2.data_ptr(), vo2.data_ptr(),
+                                   stream()) == 0
+        torch.cuda.synchronize()
+        assert_bytes_equal(u8(qr), u8(qr2), "row bytes vs reference kernel")
+        assert_f32_bitexact(f32(sr), f32(sr2), "row scales vs reference kernel")
+        assert_bytes_equal(u8(qc)[:P], u8(qc2)[:P], "col bytes vs reference kernel")
+        assert_f32_bitexact(f32(sc)[: P // 128], f32(sc2)[: P // 128], "col scales vs reference kernel")
+
+
+# ---------------------------------------------------------------------------
+# MXFP8 (rule restated from the OCP MX spec; the reference kernel is absent)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(256, 512), (176, 160), (64, 32), (2, 96, 256)])
+@pytest.mark.parametrize("qdt", FP8)
+@pytest.mark.parametrize("use_2d", [False, True])
+def test_mxfp8_vs_oracle(shape, qdt, use_2d):
+    turbo, SG, SR = _turbo()
+    g = torch.Generator().manual_seed(8)
+    mag = torch.exp(torch.randn(shape, generator=g) * 1.5)
+    sign = torch.where(torch.rand(shape, generator=g) < 0.5, -1.0, 1.0)
+    x = (mag * sign).to(torch.bfloat16)
+    r = SR(use_2d_block=use_2d)
+    nd = len(shape)
+    for direction, axis in ((1, nd - 1), (0, nd - 2)):
+        q, e = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.MX_BLOCKWISE, block_size=32, axis=axis, scaling_recipe=r)
+        qo, eo = O.quant_mx(x, FMT[qdt], direction, use_2d)
+        assert e.dtype == torch.float8_e8m0fnu
+        assert_bytes_equal(u8(q), qo, f"mx bytes dir={direction}")
+        assert_bytes_equal(u8(e), eo, f"e8m0 dir={direction}")
+    if nd == 2:
+        qr, er, qc, ec = turbo.ops.quantize_fp8_with_trans(x.cuda(), qdt, SG.MX_BLOCKWISE, block_size=32,
+                                                          scaling_recipe=r, scaling_recipe_for_trans=r)
+        assert_bytes_equal(u8(qr), O.quant_mx(x, FMT[qdt], 1, use_2d)[0], "dual row bytes")
+        assert_bytes_equal(u8(qc), O.quant_mx(x, FMT[qdt], 0, use_2d)[0], "dual col bytes")
+
+
+# ---------------------------------------------------------------------------
+# dequantization
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("qdt", FP8)
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_dequant_vs_oracle(qdt, out):
+    turbo, SG, SR = _turbo()
+    x = _input((300, 260), seed=9)
+    xc = x.cuda()
+    # tensorwise
+    q, s = turbo.ops.quantize_fp8(xc, qdt, SG.TENSORWISE)
+    y = turbo.ops.dequantize_fp8(q, out, SG.TENSORWISE, scale_inv=s)
+    ref = O.dequant_tensorwise(u8(q), FMT[qdt], f32(s))
+    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+    # blockwise 1-D both axes and 2-D
+    for axis in (0, 1):
+        q, s = turbo.ops.quantize_fp8(xc, qdt, SG.BLOCKWISE, block_size=128, axis=axis)
+        y = turbo.ops.dequantize_fp8(q, out, SG.BLOCKWISE, block_size=128, axis=axis, scale_inv=s)
+        ref = O.dequant_block1d(u8(q), FMT[qdt], f32(s), axis)
+        np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+    r = SR(use_2d_block=True)
+    q, s = turbo.ops.quantize_fp8(xc, qdt, SG.BLOCKWISE, block_size=128, scaling_recipe=r)
+    y = turbo.ops.dequantize_fp8(q, out, SG.BLOCKWISE, block_size=128, scale_inv=s, scaling_recipe=r)
+    ref = O.dequant_block2d(u8(q), FMT[qdt], f32(s))
+    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+    # rowwise
+    q, s = turbo.ops.quantize_fp8(xc, qdt, SG.ROWWISE, axis=-1)
+    y = turbo.ops.dequantize_fp8(q, out, SG.ROWWISE, axis=-1, scale_inv=s)
+    ref = O.dequant_rowwise(u8(q), FMT[qdt], f32(s))
+    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+
+
+def test_reference_roundtrip_tolerance():
+    """The reference's own quantize->dequantize criterion (tests/pytorch/ops/
+    test_quantization.py with tests/pytorch/test_utils.py:17-31: rtol = atol = 0.1)."""
+    turbo, SG, SR = _turbo()
+    x = randn((512, 1024), seed=10).cuda()
+    for g, kw in ((SG.TENSORWISE, {}), (SG.ROWWISE, {"axis": -1}), (SG.BLOCKWISE, {"block_size": 128, "axis": 1})):
+        q, s = turbo.ops.quantize_fp8(x, torch.float8_e4m3fn, g, **kw)
+        y = turbo.ops.dequantize_fp8(q, torch.bfloat16, g, scale_inv=s, **kw)
+        torch.testing.assert_close(y, x, rtol=0.1, atol=0.1)
