@@ -1,0 +1,255 @@
+"""Benchmark of the FP8 linear path on one MI355X (BASELINE.json metric:
+"FP8 GEMM TFLOP/s (% of FP8 MFMA peak); quantize GB/s (% HBM), 1 GPU").
+
+Workload (the north-star configuration, BASELINE.json configs[2] shape S1):
+DeepSeek-V3-style blockwise FP8 -- activations 1x128 scales, weights 128x128
+scales, e4m3, M=4096, K=7168, N=18432, bf16 inputs N(0,1) with 0.1% outliers x50.
+
+A step is one forward blockwise GEMM (gemm_fp8 NT kernel) on operands already
+quantized and resident in HBM; `value` is 2*M*N*K / (time per step).  The
+same run also times the quantize kernels of that workload (activation dual
+quantization, 128x128 weight quantization) and the full forward + backward
+of gemm_fp8 (quantize + NT fwd + dgrad + wgrad), reported as extra fields.
+
+Roofline: the dominant kernel is the GEMM (MFMA-bound); peak = 5.0 PFLOP/s
+dense FP8 (MI355X).  The quantize kernels are HBM-bound, peak 8 TB/s.
+
+cpu_baseline: the CPU oracle (oracle/oracle.py: fp64 product of the
+dequantized operands, numpy/BLAS threads) on a bounded row sample of the same
+GEMM, scaled to TFLOP/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "primus-turbo_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP8_TFLOPS = 5000.0  # dense FP8 MFMA, MI355X
+PEAK_HBM_GBS = 8000.0     # HBM3E, MI355X
+
+
+def _time_cuda(fn, steps: int, warmup: int):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per call (events on the launch stream)
+
+
+def _traffic_from_profiles(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/<name>.txt), if present."""
+    path = os.path.join(ROOT, "profiles", f"{name}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("hbm_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1])
+            except ValueError:
+                return None
+    return None
+
+
+def _cpu_baseline(M, N, K, seed_inputs):
+    """Oracle GEMM on a row sample (fp64 BLAS over dequantized operands)."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    a_q, a_s, w_q, w_s = seed_inputs
+    rows = 256
+    t0 = time.perf_counter()
+    da = O.dequant_block1d(a_q[:rows], 0, a_s[:rows], 1)
+    dw = O.dequant_block2d(w_q, 0, w_s)
+    t1 = time.perf_counter()
+    _ = O.gemm_ref(da, dw, False, True)
+    t2 = time.perf_counter()
+    flops = 2.0 * rows * N * K
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    return {
+        "value": flops / (t2 - t0) / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(cores),
+        "kind": "port",
+        "sample": f"{rows} of {M} rows: dequantize ({t1 - t0:.2f} s) + fp64 BLAS matmul ({t2 - t1:.2f} s) "
+                  f"of the [{rows}x{K}] x [{N}x{K}]^T blockwise GEMM",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the FP8 linear path is benchmarked on a "
+                                   "single MI355X (multi-GPU sharding is a design note, not a run)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import (
+        Float8QuantConfig,
+        Format,
+        ScalingGranularity,
+        ScalingRecipe,
+    )
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_nt
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_dual_impl,
+        quant_fp8_blockwise_for_weight_impl,
+    )
+
+    M, K, N = 4096, 7168, 18432
+    dev = "cuda:0"
+    g = torch.Generator().manual_seed(0)
+
+    def outl(shape, scale=1.0):
+        x = torch.randn(shape, generator=g) * scale
+        n = x.numel()
+        idx = torch.randperm(n, generator=g)[: n // 1000]
+        x.view(-1)[idx] *= 50.0
+        return x.to(torch.bfloat16)
+
+    a = outl((M, K)).to(dev)
+    w = outl((N, K)).to(dev)
+    grad = outl((M, N)).to(dev)
+    fdt = torch.float8_e4m3fn
+    SG = ScalingGranularity
+
+    # ---- quantized operands (resident in HBM) ------------------------------
+    a_row, a_s, _, _ = quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True)
+    w_q, w_s = quant_fp8_blockwise_for_weight_impl(w, fdt, 128)
+    nbk = K // 128
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def gemm():
+        gemm_fp8_nt(a_row, w_q, torch.bfloat16, SG.BLOCKWISE, a_s, (nbk, 1), False, w_s, (nbk, 1), True, out=out)
+
+    ms = _time_cuda(gemm, args.steps, args.warmup)
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    # ---- quantize kernels ----------------------------------------------------
+    def q_act():
+        quant_fp8_blockwise_dual_impl(a, fdt, 128)
+
+    def q_w():
+        quant_fp8_blockwise_for_weight_impl(w, fdt, 128)
+
+    qa_ms = _time_cuda(q_act, max(args.steps, 20), 5)
+    qw_ms = _time_cuda(q_w, max(args.steps, 20), 5)
+    qa_bytes = M * K * (2 + 1 + 1) + 4 * (M * (K // 128) + (M // 128) * K)
+    qw_bytes = N * K * (2 + 1) + 4 * (N // 128) * (K // 128)
+    qa_gbs = qa_bytes / (qa_ms * 1e-3) / 1e9
+    qw_gbs = qw_bytes / (qw_ms * 1e-3) / 1e9
+
+    # ---- full forward + backward of gemm_fp8 -------------------------------
+    cfg = Float8QuantConfig(granularity=SG.BLOCKWISE, format=Format.E4M3, block_size=128)
+    a_p = a.detach().requires_grad_()
+    w_p = w.detach().requires_grad_()
+
+    def train_step():
+        a_p.grad = None
+        w_p.grad = None
+        o = turbo.ops.gemm_fp8(a_p, w_p, trans_b=True, config=cfg)
+        o.backward(grad)
+
+    step_ms = _time_cuda(train_step, max(3, args.steps // 5), 2)
+
+    # ---- layouts of the backward GEMMs, timed alone -------------------------
+    g_row, g_s, g_colT, g_cs = quant_fp8_blockwise_dual_impl(grad, fdt, 128, col_transposed=True)
+    _, _, a_colT, a_cs = quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True)
+    _, _, w_t = quant_fp8_blockwise_for_weight_impl(w, fdt, 128, with_transpose=True)
+    da = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    dw = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    nbn = N // 128
+
+    def dgrad():
+        gemm_fp8_nt(g_row, w_t, torch.bfloat16, SG.BLOCKWISE, g_s, (nbn, 1), False, w_s, (1, nbk), True, out=da)
+
+    def wgrad():
+        gemm_fp8_nt(g_colT, a_colT, torch.bfloat16, SG.BLOCKWISE, g_cs, (1, N), False, a_cs, (1, K), False, out=dw)
+
+    dg_ms = _time_cuda(dgrad, max(5, args.steps // 2), 3)
+    wg_ms = _time_cuda(wgrad, max(5, args.steps // 2), 3)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_baseline(
+            M, N, K,
+            (a_row[:256].cpu().view(torch.uint8).numpy(), a_s[:256].cpu().numpy(),
+             w_q.cpu().view(torch.uint8).numpy(), w_s.cpu().numpy()),
+        )
+
+    traffic = _traffic_from_profiles("gemm_blockwise_nt_4096x18432x7168_traffic")
+    line = {
+        "metric": "FP8 GEMM TFLOP/s (% of FP8 MFMA peak); quantize GB/s (% HBM), 1 GPU",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate, bf16 out)",
+        "data": "synthetic (seeded N(0,1) bf16 with 0.1% outliers x50)",
+        "config": {
+            "workload": "blockwise FP8 gemm_fp8 forward NT (1x128 act / 128x128 weight scales, e4m3)",
+            "M": M, "N": N, "K": K, "baseline_config_index": 2,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_FP8_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_FP8_TFLOPS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "quantize": {
+            "act_dual_1x128": {"ms": round(qa_ms, 4), "GB/s": round(qa_gbs, 1), "frac_hbm": round(qa_gbs / PEAK_HBM_GBS, 4),
+                               "algorithmic_bytes": qa_bytes},
+            "weight_128x128": {"ms": round(qw_ms, 4), "GB/s": round(qw_gbs, 1), "frac_hbm": round(qw_gbs / PEAK_HBM_GBS, 4),
+                               "algorithmic_bytes": qw_bytes},
+        },
+        "backward_gemms": {
+            "dgrad_NT_on_transposed_weight": {"ms": round(dg_ms, 4), "TFLOP/s": round(flops / dg_ms / 1e9, 1)},
+            "wgrad_NT_on_transposed_columns": {"ms": round(wg_ms, 4), "TFLOP/s": round(flops / wg_ms / 1e9, 1)},
+        },
+        "fwd_bwd_step": {"ms": round(step_ms, 4), "TFLOP/s": round(3 * flops / step_ms / 1e9, 1),
+                         "includes": "quantize a/w/grad + fwd + dgrad + wgrad"},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -8,14 +8,19 @@
 //   MX          scaled MFMA with E8M0 per 32-K block (turbo_gemm_mxfp8_kernel.h:495-863)
 // Other layouts (NN / TN / trans_c) are reduced to NT on the host side.
 //
-// Tiling: 512 lanes (8 waves, 2 per SIMD), block tile 256 x 256 x 128, wave
-// tile 64 (M) x 128 (N).  The MFMA is issued "transposed": its first operand
-// is the B tile (rows n) and its second the A tile (rows m), so that lane l
-// holds C[m = l%16][n = 4*(l/16) .. +3] of each 16 x 16 sub-tile: one A row
-// per lane (one A scale per sub-tile) and four consecutive n (8-byte bf16
-// stores).  Operands are staged global -> VGPR -> LDS (2 stages, 128 KB) with
-// an XOR swizzle of the 16-byte chunk index so that both the row-wise stores
-// and the MFMA fragment reads are bank-conflict free.
+// Tiling: block tile BM x BN x 128 over WGM x WGN waves, wave tile 64 (M) x
+// 128 (N) = 4 x 8 MFMA sub-tiles.  The MFMA is issued "transposed": its first
+// operand is the B tile (rows n) and its second the A tile (rows m), so lane l
+// holds C[m = l%16][n = 4*(l/16) .. +3] of each 16 x 16 sub-tile: one A row per
+// lane (one A scale per sub-tile) and four consecutive n (8-byte bf16 stores).
+//
+// Operands go global -> LDS with buffer_load_dwordx4 ... lds (no staging
+// VGPRs), double-buffered; the 16-byte chunk index of each 128-byte tile row
+// is XOR-swizzled (chosen on the global side, since lane i of an LDS-DMA
+// always lands at M0 + 16 i) so the MFMA fragment reads are conflict free.
+// Blockwise: each K block's MFMA writes a fresh partial that is scaled into
+// the fp32 accumulator by VALU FMAs two MFMAs later, so the VALU work
+// (4 FMAs per MFMA) overlaps the matrix pipe.
 #pragma once
 #include "common.h"
 
@@ -26,13 +31,15 @@ typedef int   v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 256, BN = 256, BK = 128;
-constexpr int NTHR = 512;
-constexpr int WGM = 4, WGN = 2;           // wave grid
-constexpr int WTM = BM / WGM;             // 64
-constexpr int WTN = BN / WGN;             // 128
+constexpr int WGM = 4, WGN = 2;             // wave grid
+constexpr int NWAVES = WGM * WGN;
+constexpr int NTHR = 64 * NWAVES;
+constexpr int WTM = BM / WGM;               // 64
+constexpr int WTN = BN / WGN;               // 128
 constexpr int TM = WTM / 16, TN = WTN / 16; // 4 x 8 MFMA sub-tiles per wave
-constexpr int TILE_BYTES = BM * BK;       // 32 KB per operand per stage
-constexpr int CHUNKS_PER_THR = TILE_BYTES / 16 / NTHR; // 4
+constexpr int TILE_A_BYTES = BM * BK;
+constexpr int TILE_B_BYTES = BN * BK;
+constexpr int STAGE_BYTES  = TILE_A_BYTES + TILE_B_BYTES;
 
 enum : int { SM_TENSOR = 0, SM_ROW = 1, SM_BLOCK = 2, SM_MX = 3 };
 
@@ -118,15 +125,43 @@ __device__ __forceinline__ v8i frag(const uint8_t *base, int off0, int off1) {
     return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// buffer descriptor as an SGPR quad for inline asm (wave-uniform inputs)
+__device__ __forceinline__ v4i make_desc(const void *p, int64_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const int32_t  n = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int32_t>(bytes);
+    return v4i{__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a))),
+               __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffff)),
+               __builtin_amdgcn_readfirstlane(n), 0x00020000};
+}
+
+// 16 bytes per lane from desc[voff + soff] into LDS at m0 + 16 * lane.  The
+// instruction is hidden from the compiler's wait-count tracking on purpose:
+// completion is awaited explicitly (vmcnt(0) before the stage barrier).
+__device__ __forceinline__ void dma16(uint32_t lds_addr, int voff, v4i desc, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(desc),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void wait_dma_and_barrier() {
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT>
 __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    // LDS byte address of the dynamic shared buffer (M0 operand of the DMA)
+    const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)(__attribute__((address_space(3))) uint8_t *)(smem));
 
     const int t    = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int wm   = wave / WGN; // 0..3
-    const int wn   = wave % WGN; // 0..1
+    const int wm   = wave / WGN;
+    const int wn   = wave % WGN;
 
     // ---- tile scheduling -----------------------------------------------------
     int64_t        m0, n0;
@@ -136,7 +171,6 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     void          *C  = g.c;
     int64_t        kb_base = 0; // first global K block of this problem (group_mode 2)
     if (g.group_mode == 1) {
-        // tile id -> (m tile within the concatenated per-group tile list, n tile)
         const int64_t id = blockIdx.x;
         const int64_t mt = id / g.tiles_n, tn = id % g.tiles_n;
         int64_t       cum = 0, grp = -1, gstart = 0, gend = 0;
@@ -176,42 +210,41 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     }
     const int nk = static_cast<int>((K + BK - 1) / BK);
 
-    // ---- global loads: buffer resources cover exactly the valid rows, so
-    // rows past M / N read as zero; chunk c = i*NTHR + t -> (row c/8, chunk c%8)
-    const rsrc_t rA = make_rsrc(A + m0 * g.lda, (min<int64_t>(M - m0, BM) - 1) * g.lda + K);
-    const rsrc_t rB = make_rsrc(B + n0 * g.ldb, (min<int64_t>(N - n0, BN) - 1) * g.ldb + K);
-    const int    lrow = t >> 3, lch = t & 7;
-    const int    voA  = lrow * static_cast<int>(g.lda) + lch * 16;
-    const int    voB  = lrow * static_cast<int>(g.ldb) + lch * 16;
-    const int    stepA = 64 * static_cast<int>(g.lda), stepB = 64 * static_cast<int>(g.ldb);
-    const int    sw0   = lds_off(lrow, lch); // rows lrow + 64 i share the swizzle of lrow
-    const bool   ktail = (K % BK) != 0;
-
-    uint4 ra_[CHUNKS_PER_THR], rb_[CHUNKS_PER_THR];
-    auto gload = [&](int kb) {
-        const int k0 = kb * BK;
-        if (!ktail || kb + 1 < nk) {
+    // ---- LDS-DMA addressing -----------------------------------------------------
+    // wave w loads rows [w*RPW, (w+1)*RPW) of each operand tile, 8 rows per
+    // instruction; lane i fills LDS chunk i of that 1 KB span = row i/8,
+    // physical chunk i%8, which holds logical chunk (i%8) ^ swz(row).
+    constexpr int RPW_A = BM / NWAVES, RPW_B = BN / NWAVES;
+    constexpr int DA = RPW_A / 8, DB = RPW_B / 8;
+    const v4i  dA = make_desc(A + m0 * g.lda, (min<int64_t>(M - m0, BM) - 1) * g.lda + K);
+    const v4i  dB = make_desc(B + n0 * g.ldb, (min<int64_t>(N - n0, BN) - 1) * g.ldb + K);
+    const int  lr = lane >> 3, lp = lane & 7;
+    const int  ch_even = lp ^ lr;       // rows with (row >> 3) even
+    const int  ch_odd  = lp ^ lr ^ 1;   // rows with (row >> 3) odd
+    const int  rowA0 = wave * RPW_A + lr, rowB0 = wave * RPW_B + lr;
+    int vA[DA], vB[DB];
 #pragma unroll
-            for (int i = 0; i < CHUNKS_PER_THR; ++i) {
-                ra_[i] = bload16(rA, voA + i * stepA, k0);
-                rb_[i] = bload16(rB, voB + i * stepB, k0);
-            }
-        } else {
-            const bool ok = k0 + lch * 16 + 16 <= K;
+    for (int d = 0; d < DA; ++d) vA[d] = (rowA0 + 8 * d) * static_cast<int>(g.lda) + 16 * ((d & 1) ? ch_odd : ch_even);
 #pragma unroll
-            for (int i = 0; i < CHUNKS_PER_THR; ++i) {
-                ra_[i] = ok ? bload16(rA, voA + i * stepA, k0) : make_uint4(0, 0, 0, 0);
-                rb_[i] = ok ? bload16(rB, voB + i * stepB, k0) : make_uint4(0, 0, 0, 0);
-            }
+    for (int d = 0; d < DB; ++d) vB[d] = (rowB0 + 8 * d) * static_cast<int>(g.ldb) + 16 * ((d & 1) ? ch_odd : ch_even);
+    const bool ktail = (K % BK) != 0;
+    auto issue = [&](int kb, int stage) {
+        const int      k0 = kb * BK;
+        const uint32_t la = lds0 + stage * STAGE_BYTES + wave * RPW_A * BK;
+        const uint32_t lb = lds0 + stage * STAGE_BYTES + TILE_A_BYTES + wave * RPW_B * BK;
+        // chunks past K (last block only) read out of range and land as zeros
+        const bool last = ktail && kb + 1 == nk;
+#pragma unroll
+        for (int d = 0; d < DA; ++d) {
+            int v = vA[d];
+            if (last && k0 + 16 * ((d & 1) ? ch_odd : ch_even) >= K) v = 0x7fffffff - 64;
+            dma16(la + d * 8 * BK, v, dA, k0);
         }
-    };
-    auto swrite = [&](int s) {
-        uint8_t *sa = smem + s * TILE_BYTES;
-        uint8_t *sb = smem + (2 + s) * TILE_BYTES;
 #pragma unroll
-        for (int i = 0; i < CHUNKS_PER_THR; ++i) {
-            *reinterpret_cast<uint4 *>(sa + sw0 + i * 64 * BK) = ra_[i];
-            *reinterpret_cast<uint4 *>(sb + sw0 + i * 64 * BK) = rb_[i];
+        for (int d = 0; d < DB; ++d) {
+            int v = vB[d];
+            if (last && k0 + 16 * ((d & 1) ? ch_odd : ch_even) >= K) v = 0x7fffffff - 64;
+            dma16(lb + d * 8 * BK, v, dB, k0);
         }
     };
 
@@ -219,7 +252,7 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     const int fr   = lane & 15;
     const int fg   = lane >> 4;
     const int aoff0 = lds_off(wm * WTM + fr, fg), aoff1 = lds_off(wm * WTM + fr, 4 + fg);
-    const int boff0 = lds_off(wn * WTN + fr, fg), boff1 = lds_off(wn * WTN + fr, 4 + fg);
+    const int boff0 = TILE_A_BYTES + lds_off(wn * WTN + fr, fg), boff1 = TILE_A_BYTES + lds_off(wn * WTN + fr, 4 + fg);
 
     v4f acc[TN][TM];
 #pragma unroll
@@ -253,84 +286,121 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
             for (int j = 0; j < TN; ++j) sb_vo[j] = static_cast<int>((nbase + 16 * j + 4 * fg) * g.sb_m) * 4;
         }
     }
-
-    // ---- prologue ---------------------------------------------------------
-    gload(0);
-    swrite(0);
-    __syncthreads();
-
-    for (int kb = 0; kb < nk; ++kb) {
-        const int cur = kb & 1;
-        if (kb + 1 < nk) gload(kb + 1);
-
-        // per-K-block scales
-        float sa_r[TM];
-        float sb_u = 1.0f;
-        float sb_r[TN][4];
-        int   ea_r[TM], eb_r[TN];
+    // scales of one K block (loaded one block ahead)
+    struct Scales {
+        float sa[TM];
+        float sb_u;
+        float sb[TN][4];
+        int   ea[TM], eb[TN];
+    };
+    auto load_scales = [&](int kb, Scales &s) {
         if constexpr (SM == SM_BLOCK) {
             const int ka  = static_cast<int>((kb + kb_base) * g.sa_k) * 4;
             const int kbb = static_cast<int>((kb + kb_base) * g.sb_k) * 4;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) sa_r[i] = bload_f32(rSA, sa_vo[i], ka);
+            for (int i = 0; i < TM; ++i) s.sa[i] = bload_f32(rSA, sa_vo[i], ka);
             if constexpr (B2D) {
-                sb_u = bload_f32(rSB, sb_uo, kbb);
+                s.sb_u = bload_f32(rSB, sb_uo, kbb);
             } else {
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     if (g.sb_m == 1 && nbase + 16 * j + 4 * fg + 4 <= N) {
                         const float4 q = bload_f32x4(rSB, sb_vo[j], kbb);
-                        sb_r[j][0] = q.x; sb_r[j][1] = q.y; sb_r[j][2] = q.z; sb_r[j][3] = q.w;
+                        s.sb[j][0] = q.x; s.sb[j][1] = q.y; s.sb[j][2] = q.z; s.sb[j][3] = q.w;
                     } else {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) sb_r[j][r] = bload_f32(rSB, sb_vo[j] + r * static_cast<int>(g.sb_m) * 4, kbb);
+                        for (int r = 0; r < 4; ++r) s.sb[j][r] = bload_f32(rSB, sb_vo[j] + r * static_cast<int>(g.sb_m) * 4, kbb);
                     }
                 }
             }
         } else if constexpr (SM == SM_MX) {
             const int kk = static_cast<int>((kb + kb_base) * 4) + fg;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) ea_r[i] = bload_u8(rSA, sa_vo[i] + kk, 0);
+            for (int i = 0; i < TM; ++i) s.ea[i] = bload_u8(rSA, sa_vo[i] + kk, 0);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) eb_r[j] = bload_u8(rSB, sb_vo[j] + kk, 0);
+            for (int j = 0; j < TN; ++j) s.eb[j] = bload_u8(rSB, sb_vo[j] + kk, 0);
         }
+    };
 
-        const uint8_t *As = smem + cur * TILE_BYTES;
-        const uint8_t *Bs = smem + (2 + cur) * TILE_BYTES;
+    // ---- prologue ---------------------------------------------------------
+    Scales sc_cur{}, sc_nxt{};
+    if (nk > 0) {
+        load_scales(0, sc_cur);
+        issue(0, 0);
+    }
+    wait_dma_and_barrier();
+
+    // blockwise pipeline state: partial buffers p[4]; the two tiles issued last
+    // in a K block are scaled at the start of the next one with that block's scales
+    v4f   p[4];
+    float s_pend[4];
+    bool  have_pend = false;
+
+    for (int kb = 0; kb < nk; ++kb) {
+        const int cur = kb & 1;
+        if (kb + 1 < nk) {
+            load_scales(kb + 1, sc_nxt);
+            issue(kb + 1, cur ^ 1);
+        }
+        const uint8_t *S = smem + cur * STAGE_BYTES;
         v8i            af[TM];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) af[i] = frag(As, aoff0 + i * 16 * BK, aoff1 + i * 16 * BK);
+        for (int i = 0; i < TM; ++i) af[i] = frag(S, aoff0 + i * 16 * BK, aoff1 + i * 16 * BK);
         float s_i[TM];
         if constexpr (SM == SM_BLOCK && B2D) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) s_i[i] = sa_r[i] * sb_u;
+            for (int i = 0; i < TM; ++i) s_i[i] = sc_cur.sa[i] * sc_cur.sb_u;
         }
+        v8i bf = frag(S, boff0, boff1);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const v8i bf = frag(Bs, boff0 + j * 16 * BK, boff1 + j * 16 * BK);
+            v8i bn = bf;
+            if (j + 1 < TN) bn = frag(S, boff0 + (j + 1) * 16 * BK, boff1 + (j + 1) * 16 * BK);
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
+                const int tt = j * TM + i;
                 if constexpr (SM == SM_BLOCK) {
-                    const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    p[tt & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                         bf, af[i], v4f{0.f, 0.f, 0.f, 0.f}, FB, FA, 0, 0, 0, 0);
+                    // scale the tile issued two MFMAs earlier
                     if constexpr (B2D) {
-                        acc[j][i] += p * s_i[i];
+                        if (tt >= 2) {
+                            const int q = tt - 2;
+                            acc[q / TM][q % TM] += p[q & 3] * s_i[q % TM];
+                        } else if (have_pend) {
+                            const int q = TN * TM - 2 + tt; // tiles 30, 31 of the previous block
+                            acc[q / TM][q % TM] += p[q & 3] * s_pend[q & 3];
+                        }
                     } else {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[j][i][r] += p[r] * (sa_r[i] * sb_r[j][r]);
+                        for (int r = 0; r < 4; ++r) acc[j][i][r] += p[tt & 3][r] * (sc_cur.sa[i] * sc_cur.sb[j][r]);
                     }
                 } else if constexpr (SM == SM_MX) {
                     acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        bf, af[i], acc[j][i], FB, FA, 0, eb_r[j], 0, ea_r[i]);
+                        bf, af[i], acc[j][i], FB, FA, 0, sc_cur.eb[j], 0, sc_cur.ea[i]);
                 } else {
                     acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                         bf, af[i], acc[j][i], FB, FA, 0, 0, 0, 0);
                 }
             }
+            bf = bn;
         }
-
-        if (kb + 1 < nk) swrite(cur ^ 1);
-        __syncthreads();
+        if constexpr (SM == SM_BLOCK && B2D) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s_pend[q] = s_i[q % TM];
+            have_pend = true;
+        }
+        sc_cur = sc_nxt;
+        wait_dma_and_barrier();
+    }
+    if constexpr (SM == SM_BLOCK && B2D) {
+        if (have_pend) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int q = TN * TM - 2 + tt;
+                acc[q / TM][q % TM] += p[q & 3] * s_pend[q & 3];
+            }
+        }
     }
 
     // ---- epilogue -----------------------------------------------------------
@@ -370,7 +440,7 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     }
 }
 
-constexpr size_t SMEM_BYTES = 4 * TILE_BYTES; // 128 KB
+constexpr size_t SMEM_BYTES = 2 * STAGE_BYTES; // two stages
 
 template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT>
 int launch_one(const GemmArgs &g, hipStream_t st) {
