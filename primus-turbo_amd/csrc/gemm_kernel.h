@@ -66,7 +66,9 @@ struct GemmArgs {
     int64_t        b_gstride, sb_gstride, c_gstride; // elements / bytes per group
 };
 
-__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+// gfx950 serves a ds_read_b128 two 8-lane groups per clock; with the chunk
+// XORed by row % 8 the 16-row fragment reads hit every bank once per clock.
+__device__ __forceinline__ int swz(int row) { return row & 7; }
 
 // byte offset of logical 16-byte chunk `ch` of tile row `row`
 __device__ __forceinline__ int lds_off(int row, int ch) { return row * BK + ((ch ^ swz(row)) << 4); }
@@ -219,14 +221,13 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     const v4i  dA = make_desc(A + m0 * g.lda, (min<int64_t>(M - m0, BM) - 1) * g.lda + K);
     const v4i  dB = make_desc(B + n0 * g.ldb, (min<int64_t>(N - n0, BN) - 1) * g.ldb + K);
     const int  lr = lane >> 3, lp = lane & 7;
-    const int  ch_even = lp ^ lr;       // rows with (row >> 3) even
-    const int  ch_odd  = lp ^ lr ^ 1;   // rows with (row >> 3) odd
+    const int  ch = lp ^ lr;            // rows of one DMA are 8 apart: same swizzle
     const int  rowA0 = wave * RPW_A + lr, rowB0 = wave * RPW_B + lr;
     int vA[DA], vB[DB];
 #pragma unroll
-    for (int d = 0; d < DA; ++d) vA[d] = (rowA0 + 8 * d) * static_cast<int>(g.lda) + 16 * ((d & 1) ? ch_odd : ch_even);
+    for (int d = 0; d < DA; ++d) vA[d] = (rowA0 + 8 * d) * static_cast<int>(g.lda) + 16 * ch;
 #pragma unroll
-    for (int d = 0; d < DB; ++d) vB[d] = (rowB0 + 8 * d) * static_cast<int>(g.ldb) + 16 * ((d & 1) ? ch_odd : ch_even);
+    for (int d = 0; d < DB; ++d) vB[d] = (rowB0 + 8 * d) * static_cast<int>(g.ldb) + 16 * ch;
     const bool ktail = (K % BK) != 0;
     auto issue = [&](int kb, int stage) {
         const int      k0 = kb * BK;
@@ -237,13 +238,13 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
 #pragma unroll
         for (int d = 0; d < DA; ++d) {
             int v = vA[d];
-            if (last && k0 + 16 * ((d & 1) ? ch_odd : ch_even) >= K) v = 0x7fffffff - 64;
+            if (last && k0 + 16 * ch >= K) v = 0x7fffffff - 64;
             dma16(la + d * 8 * BK, v, dA, k0);
         }
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
             int v = vB[d];
-            if (last && k0 + 16 * ((d & 1) ? ch_odd : ch_even) >= K) v = 0x7fffffff - 64;
+            if (last && k0 + 16 * ch >= K) v = 0x7fffffff - 64;
             dma16(lb + d * 8 * BK, v, dB, k0);
         }
     };
