@@ -40,6 +40,15 @@ constexpr int TM = WTM / 16, TN = WTN / 16; // 4 x 8 MFMA sub-tiles per wave
 constexpr int TILE_A_BYTES = BM * BK;
 constexpr int TILE_B_BYTES = BN * BK;
 constexpr int STAGE_BYTES  = TILE_A_BYTES + TILE_B_BYTES;
+// per-column B scales of one K block (1-D x 1-D blockwise), one slot per stage
+constexpr int SCALE_SLOT   = BN * 4;
+constexpr int SCALE_BASE   = 2 * STAGE_BYTES;
+// epilogue: the C tile is staged in LDS as 16-bit rows padded by 16 bytes, so
+// the per-lane 8-byte writes of 16 consecutive rows hit distinct banks
+constexpr int EPI_PITCH    = BN * 2 + 16;
+constexpr int EPI_BYTES    = BM * EPI_PITCH;
+constexpr int MAIN_BYTES   = SCALE_BASE + 2 * SCALE_SLOT;
+constexpr size_t SMEM_BYTES = EPI_BYTES > MAIN_BYTES ? EPI_BYTES : MAIN_BYTES;
 
 enum : int { SM_TENSOR = 0, SM_ROW = 1, SM_BLOCK = 2, SM_MX = 3 };
 
@@ -149,6 +158,15 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, int voff, v4i desc, int
                  : "memory", "m0");
 }
 
+// 4 bytes per lane from desc[voff + soff] into LDS at m0 + 4 * lane
+__device__ __forceinline__ void dma4(uint32_t lds_addr, int voff, v4i desc, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(desc),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
+                 : "memory", "m0");
+}
+
 __device__ __forceinline__ void wait_dma_and_barrier() {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 }
@@ -229,6 +247,9 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
 #pragma unroll
     for (int d = 0; d < DB; ++d) vB[d] = (rowB0 + 8 * d) * static_cast<int>(g.ldb) + 16 * ch;
     const bool ktail = (K % BK) != 0;
+    // 1-D B scales: lane i of wave w < 4 stages column n0 + 64 w + i
+    const v4i dSB    = make_desc(SB, g.sb_bytes);
+    const int sbl_vo = static_cast<int>((n0 + 64 * (wave & 3) + lane) * g.sb_m) * 4;
     auto issue = [&](int kb, int stage) {
         const int      k0 = kb * BK;
         const uint32_t la = lds0 + stage * STAGE_BYTES + wave * RPW_A * BK;
@@ -246,6 +267,12 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
             int v = vB[d];
             if (last && k0 + 16 * ch >= K) v = 0x7fffffff - 64;
             dma16(lb + d * 8 * BK, v, dB, k0);
+        }
+        if constexpr (SM == SM_BLOCK && !B2D) {
+            // waves 0..3 each stage 64 column scales of this K block
+            if (wave < BN / 64)
+                dma4(lds0 + SCALE_BASE + stage * SCALE_SLOT + wave * 256, sbl_vo,
+                     dSB, static_cast<int>((kb + kb_base) * g.sb_k) * 4);
         }
     };
 
@@ -282,16 +309,12 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
             for (int j = 0; j < TN; ++j) sb_vo[j] = static_cast<int>(min<int64_t>(nbase + 16 * j + fr, N - 1) * g.sb_m);
         } else if constexpr (B2D) {
             sb_uo = static_cast<int>((nbase >> 7) * g.sb_m) * 4;
-        } else {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) sb_vo[j] = static_cast<int>((nbase + 16 * j + 4 * fg) * g.sb_m) * 4;
         }
     }
     // scales of one K block (loaded one block ahead)
     struct Scales {
         float sa[TM];
         float sb_u;
-        float sb[TN][4];
         int   ea[TM], eb[TN];
     };
     auto load_scales = [&](int kb, Scales &s) {
@@ -300,20 +323,7 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
             const int kbb = static_cast<int>((kb + kb_base) * g.sb_k) * 4;
 #pragma unroll
             for (int i = 0; i < TM; ++i) s.sa[i] = bload_f32(rSA, sa_vo[i], ka);
-            if constexpr (B2D) {
-                s.sb_u = bload_f32(rSB, sb_uo, kbb);
-            } else {
-#pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    if (g.sb_m == 1 && nbase + 16 * j + 4 * fg + 4 <= N) {
-                        const float4 q = bload_f32x4(rSB, sb_vo[j], kbb);
-                        s.sb[j][0] = q.x; s.sb[j][1] = q.y; s.sb[j][2] = q.z; s.sb[j][3] = q.w;
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) s.sb[j][r] = bload_f32(rSB, sb_vo[j] + r * static_cast<int>(g.sb_m) * 4, kbb);
-                    }
-                }
-            }
+            if constexpr (B2D) s.sb_u = bload_f32(rSB, sb_uo, kbb);
         } else if constexpr (SM == SM_MX) {
             const int kk = static_cast<int>((kb + kb_base) * 4) + fg;
 #pragma unroll
@@ -353,8 +363,11 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
             for (int i = 0; i < TM; ++i) s_i[i] = sc_cur.sa[i] * sc_cur.sb_u;
         }
         v8i bf = frag(S, boff0, boff1);
+        const float *SBL = reinterpret_cast<const float *>(smem + SCALE_BASE + cur * SCALE_SLOT) + wn * WTN + 4 * fg;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
+            float4 sbj = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (SM == SM_BLOCK && !B2D) sbj = *reinterpret_cast<const float4 *>(SBL + 16 * j);
             v8i bn = bf;
             if (j + 1 < TN) bn = frag(S, boff0 + (j + 1) * 16 * BK, boff1 + (j + 1) * 16 * BK);
 #pragma unroll
@@ -373,8 +386,11 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
                             acc[q / TM][q % TM] += p[q & 3] * s_pend[q & 3];
                         }
                     } else {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[j][i][r] += p[tt & 3][r] * (sc_cur.sa[i] * sc_cur.sb[j][r]);
+                        const float sa_i = sc_cur.sa[i];
+                        acc[j][i][0] += p[tt & 3][0] * (sa_i * sbj.x);
+                        acc[j][i][1] += p[tt & 3][1] * (sa_i * sbj.y);
+                        acc[j][i][2] += p[tt & 3][2] * (sa_i * sbj.z);
+                        acc[j][i][3] += p[tt & 3][3] * (sa_i * sbj.w);
                     }
                 } else if constexpr (SM == SM_MX) {
                     acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
@@ -405,6 +421,63 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     }
 
     // ---- epilogue -----------------------------------------------------------
+    if constexpr (OUT_DT != PTA_F32) {
+        // full tiles: convert in registers, stage the 256 x 256 tile in LDS,
+        // then write whole 16-byte row segments (full cache lines per row)
+        if (g.aligned_c && m0 + BM <= M && n0 + BN <= N) {
+            typedef float ef2 __attribute__((ext_vector_type(2)));
+            float ets = 1.0f, era[TM];
+            if constexpr (SM == SM_TENSOR)
+                ets = reinterpret_cast<const float *>(g.sa)[0] * reinterpret_cast<const float *>(SB)[0];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                era[i] = 1.0f;
+                if constexpr (SM == SM_ROW) era[i] = reinterpret_cast<const float *>(g.sa)[mw + 16 * i + fr];
+            }
+            // all waves are past their last fragment reads
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                float erb[4] = {1.f, 1.f, 1.f, 1.f};
+                if constexpr (SM == SM_ROW) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) erb[r] = reinterpret_cast<const float *>(SB)[nbase + 16 * j + 4 * fg + r];
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    float x[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float v = acc[j][i][r];
+                        if constexpr (SM == SM_TENSOR) v = v * ets;
+                        if constexpr (SM == SM_ROW) v = v * era[i] * erb[r];
+                        x[r] = v;
+                    }
+                    uint32_t lo, hi;
+                    if constexpr (OUT_DT == PTA_BF16) {
+                        typedef __bf16 eb2 __attribute__((ext_vector_type(2)));
+                        lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((ef2{x[0], x[1]}), eb2));
+                        hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((ef2{x[2], x[3]}), eb2));
+                    } else {
+                        typedef _Float16 eh2 __attribute__((ext_vector_type(2)));
+                        lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((ef2{x[0], x[1]}), eh2));
+                        hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((ef2{x[2], x[3]}), eh2));
+                    }
+                    const int off = (wm * WTM + 16 * i + fr) * EPI_PITCH + (wn * WTN + 16 * j + 4 * fg) * 2;
+                    *reinterpret_cast<uint2 *>(smem + off) = make_uint2(lo, hi);
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            const int c16 = t & 31; // 16-byte column chunk; 16 rows per pass
+            uint16_t *Cb = reinterpret_cast<uint16_t *>(C) + m0 * g.ldc + n0 + 8 * c16;
+#pragma unroll 4
+            for (int q = 0; q < BM * BN * 2 / (16 * NTHR); ++q) {
+                const int r = (t >> 5) + 16 * q;
+                *reinterpret_cast<uint4 *>(Cb + r * g.ldc) = *reinterpret_cast<const uint4 *>(smem + r * EPI_PITCH + c16 * 16);
+            }
+            return;
+        }
+    }
     float ts = 1.0f;
     if constexpr (SM == SM_TENSOR) {
         ts = reinterpret_cast<const float *>(g.sa)[0] * reinterpret_cast<const float *>(SB)[0];
@@ -440,8 +513,6 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
         }
     }
 }
-
-constexpr size_t SMEM_BYTES = 2 * STAGE_BYTES; // two stages
 
 template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT>
 int launch_one(const GemmArgs &g, hipStream_t st) {
