@@ -166,6 +166,8 @@ def main():
     extras = {}
     if args.only == "all":
         extras = _extras(args, a, w, grad, M, N, K, flops)
+        del grad
+        extras["other_configs"] = _other_configs(args)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -212,6 +214,130 @@ def main():
     }
     line.update(extras)
     print(json.dumps(line))
+
+
+def _gemm_rec(ms, flops):
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_FP8_TFLOPS, 4)}
+
+
+def _quant_rec(ms, nbytes):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+            "algorithmic_bytes": int(nbytes)}
+
+
+def _zipf_counts(total, experts, nonempty, seed):
+    """BASELINE config 4 split: rank weights r^-1.1 over `nonempty` experts, the
+    rest empty, experts permuted with a seeded generator."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    w = torch.tensor([r ** -1.1 for r in range(1, nonempty + 1)], dtype=torch.float64)
+    cnt = torch.floor(total * w / w.sum()).to(torch.int64)
+    cnt[0] += total - int(cnt.sum())
+    full = torch.zeros(experts, dtype=torch.int64)
+    full[:nonempty] = cnt
+    return full[torch.randperm(experts, generator=g)]
+
+
+def _other_configs(args):
+    """The remaining BASELINE.json configurations, each timed on the GPU
+    (GEMM TFLOP/s against the dense FP8 peak, quantize GB/s against HBM)."""
+    import torch
+
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_impl, gemm_fp8_nt
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_fp8_impl import grouped_gemm_fp8_impl
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_dual_impl,
+        quant_fp8_blockwise_for_weight_impl,
+        quant_fp8_blockwise_segment_m_row_col_impl,
+        quantize_fp8_rowwise_impl,
+        quantize_fp8_tensorwise_impl,
+        quantize_mxfp8_impl,
+    )
+
+    SG = ScalingGranularity
+    dev = "cuda:0"
+    e4 = torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(1)
+    it = max(5, args.steps // 5)
+    res = {}
+
+    # config 1: tensorwise 512x1024 @ 1024x1024 (NN), launch-bound
+    a1 = torch.randn((512, 1024), generator=g).bfloat16().to(dev)
+    b1 = torch.randn((1024, 1024), generator=g).bfloat16().to(dev)
+    qa1, sa1 = quantize_fp8_tensorwise_impl(a1, e4)
+    qb1, sb1 = quantize_fp8_tensorwise_impl(b1, e4)
+    res["cfg1_tensorwise_512x1024x1024_NN"] = {
+        "quant_A": _quant_rec(_time_cuda(lambda: quantize_fp8_tensorwise_impl(a1, e4), it, 3), 3 * a1.numel() + 4),
+        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_impl(qa1, sa1, False, qb1, sb1, False, torch.bfloat16, False,
+                                                           SG.TENSORWISE.value), it, 3), 2.0 * 512 * 1024 * 1024),
+    }
+    del a1, b1, qa1, qb1
+
+    # config 2: rowwise, Llama-3-8B up-proj 8192 x 4096 @ [14336 x 4096]^T
+    a2 = torch.randn((8192, 4096), generator=g).bfloat16().to(dev)
+    w2 = (torch.randn((14336, 4096), generator=g) * 0.02).bfloat16().to(dev)
+    qa2, sa2 = quantize_fp8_rowwise_impl(a2, e4, -1)
+    qw2, sw2 = quantize_fp8_rowwise_impl(w2, e4, -1)
+    res["cfg2_rowwise_8192x14336x4096_NT"] = {
+        "quant_A": _quant_rec(_time_cuda(lambda: quantize_fp8_rowwise_impl(a2, e4, -1), it, 3),
+                              3 * a2.numel() + 4 * 8192),
+        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_impl(qa2, sa2, False, qw2, sw2, True, torch.bfloat16, False,
+                                                           SG.ROWWISE.value), it, 3), 2.0 * 8192 * 14336 * 4096),
+    }
+    del a2, w2, qa2, qw2
+
+    # config 3, shape 2: blockwise 4096 x 2048 @ [7168 x 2048]^T
+    a3 = torch.randn((4096, 2048), generator=g).bfloat16().to(dev)
+    w3 = torch.randn((7168, 2048), generator=g).bfloat16().to(dev)
+    ar3, as3, _, _ = quant_fp8_blockwise_dual_impl(a3, e4, 128, col_transposed=True)
+    wq3, ws3 = quant_fp8_blockwise_for_weight_impl(w3, e4, 128)
+    o3 = torch.empty((4096, 7168), dtype=torch.bfloat16, device=dev)
+    res["cfg3_blockwise_4096x7168x2048_NT"] = {
+        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_nt(ar3, wq3, torch.bfloat16, SG.BLOCKWISE, as3, (16, 1), False,
+                                                         ws3, (16, 1), True, out=o3), it, 3), 2.0 * 4096 * 7168 * 2048),
+    }
+    del a3, w3, ar3, wq3, o3
+
+    # config 4: grouped MoE, 32 experts, 65536 routed rows, hidden 7168, FFN 2048
+    lens = _zipf_counts(65536, 32, 28, 0).to(dev)
+    offs = group_offs_from_lens(lens)
+    a4 = torch.randn((65536, 7168), generator=g).bfloat16().to(dev)
+    w4 = (torch.randn((32, 2048, 7168), generator=g) * 0.02).bfloat16().to(dev)
+    seg = lambda: quant_fp8_blockwise_segment_m_row_col_impl(a4, e4, 128, lens, offs)  # noqa: E731
+    ar4, _, asr4, _, _, _ = seg()
+    wq4, ws4 = quant_fp8_blockwise_for_weight_impl(w4, e4, 128)
+    seg_ms = _time_cuda(seg, it, 2)
+    n4 = a4.numel()
+    res["cfg4_grouped_blockwise_moe_32x2048x7168"] = {
+        "group_lens": [int(v) for v in lens.cpu()],
+        "segment_quant_A": _quant_rec(seg_ms, n4 * (2 + 1 + 1) + 4 * (n4 // 128) * 2),
+        "weight_quant": _quant_rec(_time_cuda(lambda: quant_fp8_blockwise_for_weight_impl(w4, e4, 128), it, 2),
+                                   3 * w4.numel() + 4 * w4.numel() // 16384),
+        "grouped_gemm_fwd": _gemm_rec(_time_cuda(lambda: grouped_gemm_fp8_impl(ar4, wq4, asr4, ws4, lens, offs, False,
+                                                                              True, torch.bfloat16,
+                                                                              SG.BLOCKWISE.value), it, 2),
+                                      2.0 * 65536 * 2048 * 7168),
+    }
+    del a4, w4, ar4, wq4
+
+    # config 5: MX-FP8 (block 32, e8m0), Llama-3-70B up-proj 8192 x 8192 @ [28672 x 8192]^T
+    sign = lambda t: torch.where(torch.rand(t, generator=g) < 0.5, -1.0, 1.0)  # noqa: E731
+    a5 = (sign((8192, 8192)) * torch.exp(torch.randn((8192, 8192), generator=g) * 1.5)).bfloat16().to(dev)
+    w5 = (sign((28672, 8192)) * torch.exp(torch.randn((28672, 8192), generator=g) * 1.5)).bfloat16().to(dev)
+    qa5, ea5 = quantize_mxfp8_impl(a5, e4, 1, 32)
+    qw5, ew5 = quantize_mxfp8_impl(w5, e4, 1, 32)
+    res["cfg5_mxfp8_8192x28672x8192_NT"] = {
+        "quant_dual_A": _quant_rec(_time_cuda(lambda: quantize_mxfp8_impl(a5, e4, None, 32, with_trans=True), it, 2),
+                                   a5.numel() * (2 + 1 + 1) + 2 * a5.numel() // 32),
+        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_impl(qa5, ea5, False, qw5, ew5, True, torch.bfloat16, False,
+                                                           SG.MX_BLOCKWISE.value), it, 2), 2.0 * 8192 * 28672 * 8192),
+    }
+    return res
 
 
 def _extras(args, a, w, grad, M, N, K, flops):
