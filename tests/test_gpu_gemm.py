@@ -193,3 +193,50 @@ def test_gemm_blockwise_deterministic():
     outs = [turbo.ops.gemm_fp8(a, b, False, True, torch.bfloat16, cfg) for _ in range(5)]
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
+
+
+
+@pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
+@pytest.mark.parametrize("n", [4352, 4300])
+def test_gemm_multi_round_vs_oracle(gran, n):
+    """272 tiles (more than one round on 256 CUs); n = 4300 leaves a partial last
+    tile column and a C row stride that is not 16-byte aligned."""
+    turbo, _, _, _, SG, SR, gemm_fp8_impl = _mods()
+    g = getattr(SG, gran)
+    M, K = 4096, 256
+    qdt = torch.float8_e4m3fn
+    a = randn((M, K), seed=21).cuda()
+    b = randn((n, K), seed=22).cuda()
+    if g == SG.TENSORWISE:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g)
+        da, db = O.dequant_tensorwise(u8(qa), 0, f32(sa)), O.dequant_tensorwise(u8(qb), 0, f32(sb))
+    elif g == SG.ROWWISE:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g, axis=-1)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g, axis=-1)
+        da, db = O.dequant_rowwise(u8(qa), 0, f32(sa)), O.dequant_rowwise(u8(qb), 0, f32(sb))
+    elif g == SG.BLOCKWISE:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g, block_size=128, axis=1)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g, block_size=128, scaling_recipe=SR(use_2d_block=True))
+        da, db = O.dequant_block1d(u8(qa), 0, f32(sa), 1), O.dequant_block2d(u8(qb), 0, f32(sb))
+    else:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g, block_size=32, axis=1, scaling_recipe=SR())
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g, block_size=32, axis=1, scaling_recipe=SR())
+        da, db = O.dequant_mx(u8(qa), 0, u8(sa)), O.dequant_mx(u8(qb), 0, u8(sb))
+    out = gemm_fp8_impl(qa, sa, False, qb, sb, True, torch.bfloat16, False, g.value)
+    _check(out, O.gemm_ref(da, db, False, True), f"{gran} n={n}")
+
+
+def test_gemm_multi_round_wgrad_1d_scales():
+    """1-D x 1-D blockwise (TN, column scales staged through LDS) over 272 tiles."""
+    turbo, _, _, _, SG, SR, gemm_fp8_impl = _mods()
+    g = SG.BLOCKWISE
+    M, N, K = 4096, 4352, 256
+    a = randn((K, M), seed=23).cuda()
+    b = randn((K, N), seed=24).cuda()
+    qa, sa = turbo.ops.quantize_fp8(a, torch.float8_e4m3fn, g, block_size=128, axis=0)
+    qb, sb = turbo.ops.quantize_fp8(b, torch.float8_e4m3fn, g, block_size=128, axis=0)
+    da = O.dequant_block1d(u8(qa), 0, f32(sa), 0)
+    db = O.dequant_block1d(u8(qb), 0, f32(sb), 0)
+    out = gemm_fp8_impl(qa, sa, True, qb, sb, False, torch.bfloat16, False, g.value)
+    _check(out, O.gemm_ref(da, db, True, False), "TN multi-round")
