@@ -108,18 +108,22 @@ __device__ __forceinline__ float load_scalar(const void *base, int64_t idx) {
 }
 
 // 8 elements from a 16-byte-aligned address (two dwordx4 for fp32).
-template <int IN_DT>
+// STREAM: non-temporal loads (data read once and larger than the caches).
+template <int IN_DT, bool STREAM = false>
 __device__ __forceinline__ void load8(const void *base, int64_t idx, float (&v)[8]) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    auto ld = [](const void *p) -> v4u {
+        if constexpr (STREAM) return __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
+        else return *reinterpret_cast<const v4u *>(p);
+    };
     if constexpr (IN_DT == PTA_F32) {
-        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(base) + idx);
-        float4        a = p[0];
-        float4        b = p[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        const float *p = reinterpret_cast<const float *>(base) + idx;
+        const v4u    a = ld(p), b = ld(p + 4);
+        v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+        v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
     } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(base) + idx);
-        uint4        w = p[0];
-        uint32_t     ws[4] = {w.x, w.y, w.z, w.w};
+        const v4u w     = ld(reinterpret_cast<const uint16_t *>(base) + idx);
+        uint32_t  ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             if constexpr (IN_DT == PTA_BF16) {

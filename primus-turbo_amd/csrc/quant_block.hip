@@ -47,7 +47,7 @@ struct QBArgs {
     int64_t        G;
 };
 
-template <int IN_DT, int FMT, int MODE, bool VEC>
+template <int IN_DT, int FMT, int MODE, bool VEC, bool STREAM>
 __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     const int     t     = threadIdx.x;
     const int     lane  = t & 63;
@@ -99,8 +99,8 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         rvalid[i]       = (r >= row_lo) && (r < row_hi);
         if (VEC && rvalid[i] && n0 + 16 <= N) {
             float a[8], b[8];
-            load8<IN_DT>(xb, r * N + n0, a);
-            load8<IN_DT>(xb, r * N + n0 + 8, b);
+            load8<IN_DT, STREAM>(xb, r * N + n0, a);
+            load8<IN_DT, STREAM>(xb, r * N + n0 + 8, b);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 v[i][j]     = a[j];
@@ -352,16 +352,24 @@ __global__ __launch_bounds__(256) void offs_to_padded_offs_kernel(const int64_t 
     }
 }
 
+// Inputs larger than this are streamed with non-temporal loads: they cannot
+// stay resident in the 256 MB MALL anyway, and the hint measured 10-12% faster
+// there, while it costs as much on inputs that the MALL still holds.
+constexpr int64_t STREAM_BYTES = 192ll << 20;
+
 template <int MODE>
 int launch_tile(const QBArgs &a, int in_dtype, int fmt, dim3 grid, bool vec, hipStream_t st) {
-#define PTA_QB_LAUNCH(IDT, F, V)                                                                   \
-    quant_block_tile_kernel<IDT, F, MODE, V><<<grid, NT, 0, st>>>(a)
-#define PTA_QB_FMT(IDT, V)                                                                         \
-    if (fmt == PTA_E4M3) PTA_QB_LAUNCH(IDT, PTA_E4M3, V);                                          \
-    else PTA_QB_LAUNCH(IDT, PTA_E5M2, V)
+    const int64_t in_bytes = static_cast<int64_t>(grid.z) * a.M * a.N * (in_dtype == PTA_F32 ? 4 : 2);
+    const bool    stream   = vec && in_bytes >= STREAM_BYTES;
+#define PTA_QB_LAUNCH(IDT, F, V, S)                                                                \
+    quant_block_tile_kernel<IDT, F, MODE, V, S><<<grid, NT, 0, st>>>(a)
+#define PTA_QB_FMT(IDT, V, S)                                                                      \
+    if (fmt == PTA_E4M3) PTA_QB_LAUNCH(IDT, PTA_E4M3, V, S);                                       \
+    else PTA_QB_LAUNCH(IDT, PTA_E5M2, V, S)
 #define PTA_QB_VEC(IDT)                                                                            \
-    if (vec) { PTA_QB_FMT(IDT, true); }                                                            \
-    else { PTA_QB_FMT(IDT, false); }
+    if (stream) { PTA_QB_FMT(IDT, true, true); }                                                   \
+    else if (vec) { PTA_QB_FMT(IDT, true, false); }                                                \
+    else { PTA_QB_FMT(IDT, false, false); }
     if (in_dtype == PTA_BF16) { PTA_QB_VEC(PTA_BF16) }
     else if (in_dtype == PTA_F16) { PTA_QB_VEC(PTA_F16) }
     else { PTA_QB_VEC(PTA_F32) }

@@ -252,83 +252,124 @@ __device__ __forceinline__ float mx_qscale(int e8m0) {
     return __uint_as_float(static_cast<uint32_t>(254 - e8m0) << 23); // 2^(127 - e8m0)
 }
 
-template <int IN_DT, int FMT>
-__global__ __launch_bounds__(NT) void mx_quant_kernel(const void *x, int64_t M, int64_t N, int64_t M_pad,
-                                                       int64_t N_pad, uint8_t *q_row, uint8_t *e_row,
-                                                       int use2d_row, uint8_t *q_col, uint8_t *e_col,
-                                                       int use2d_col) {
-    const int     t  = threadIdx.x;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 64;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 64;
-    const int64_t g  = blockIdx.z;
-    const int64_t xoff = g * M * N;
+// MXFP8: one workgroup (4 waves) per 128 x 128 tile of x[g]; lane t owns rows
+// 4*(t>>3) .. +3 and columns 16*(t&7) .. +15, so one wave holds 32 consecutive
+// rows, i.e. exactly one 32-row column block, and a lane pair (t, t^1) one
+// 32-column row block:
+//   row amax (1 x 32)  = lane max, then the pair (DPP quad xor 1);
+//   col amax (32 x 1)  = max over the lane's 4 rows, then lanes ^8, ^16, ^32;
+//   2-D amax (32 x 32) = the row maxima reduced like a column.
+// Row output q_row[g*M + m, N_pad] (16-byte stores), colwise output written
+// transposed q_col[g*N + n, M_pad] through an LDS byte transpose; padded
+// elements are zero and so are their exponents.
+struct MXArgs {
+    const void *x;
+    int64_t     M, N, M_pad, N_pad;
+    uint8_t    *q_row, *e_row, *q_col, *e_col;
+    int         use2d_row, use2d_col, vec;
+};
 
-    __shared__ float s_tile[64][65];
-    __shared__ float s_bmax[2][2]; // 32x32 block maxima for the 2-D variant
-    // load: 64 rows x 64 cols, lane t: row t>>2 (+0 / +... ) handled in 4 passes of 16 rows
+template <int IN_DT, int FMT, bool ROW, bool COL, bool STREAM>
+__global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
+    const int     t    = threadIdx.x;
+    const int     wave = t >> 6;
+    const int     cseg = t & 7;
+    const int     rgrp = t >> 3;
+    const int64_t tm = blockIdx.x, tn = blockIdx.y, g = blockIdx.z;
+    const int64_t M = a.M, N = a.N;
+    const int64_t n0 = tn * 128 + cseg * 16;
+    const char   *xb = reinterpret_cast<const char *>(a.x) + g * M * N * InTraits<IN_DT>::bytes;
+
+    float v[4][16];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int     rl = p * 16 + (t >> 4);
-        const int     cl = (t & 15) * 4;
-        const int64_t m = m0 + rl;
+    for (int i = 0; i < 4; ++i) {
+        const int64_t m  = tm * 128 + rgrp * 4 + i;
+        const bool    ok = m < M && n0 < N; // N % 32 == 0: a lane's 16 columns are all in or all out
+        if (a.vec) {
+            float lo[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (ok) {
+                load8<IN_DT, STREAM>(xb, m * N + n0, lo);
+                load8<IN_DT, STREAM>(xb, m * N + n0 + 8, hi);
+            }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t n = n0 + cl + j;
-            s_tile[rl][cl + j] = (m < M && n < N) ? load_scalar<IN_DT>(x, xoff + m * N + n) : 0.0f;
+            for (int j = 0; j < 8; ++j) {
+                v[i][j]     = lo[j];
+                v[i][j + 8] = hi[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[i][j] = ok ? load_scalar<IN_DT>(xb, m * N + n0 + j) : 0.0f;
         }
     }
-    if (t < 4) s_bmax[t >> 1][t & 1] = 0.0f;
-    __syncthreads();
-    const bool need2d = (q_row && use2d_row) || (q_col && use2d_col);
-    if (need2d) {
-        // lane t: row t>>2, 16 cols ((t&3)*16): contributes to block (row/32, col/32)
-        const int rl = t >> 2, cl = (t & 3) * 16;
-        float     a  = 0.0f;
-        for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(s_tile[rl][cl + j]));
-        // non-negative floats order like their bit patterns: integer max in LDS
-        atomicMax(reinterpret_cast<int *>(&s_bmax[rl >> 5][cl >> 5]), __float_as_int(a));
+
+    // 32 x 32 block maxima (only needed by the 2-D variants)
+    float blk = 0.0f;
+    float ra[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[i][j]));
+        m     = fmaxf(m, dpp_f<PTA_DPP_QUAD_XOR1>(m));
+        ra[i] = m;
+        blk   = fmaxf(blk, m);
+    }
+    if (a.use2d_row || a.use2d_col) {
+        blk = fmaxf(blk, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(blk), 0x128, 0xf, 0xf, false)));
+        blk = fmaxf(blk, __shfl_xor(blk, 16));
+        blk = fmaxf(blk, __shfl_xor(blk, 32));
+    }
+
+    if constexpr (ROW) {
+        const int64_t eb_row = a.N_pad / 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t m = tm * 128 + rgrp * 4 + i;
+            if (m >= M) continue;
+            const int   e  = mx_e8m0<FMT>(a.use2d_row ? blk : ra[i]);
+            const float sc = mx_qscale(e);
+            uint8_t    *dst = a.q_row + (g * M + m) * a.N_pad + n0;
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(&v[i][0], sc), quant4<FMT>(&v[i][4], sc),
+                                                         quant4<FMT>(&v[i][8], sc), quant4<FMT>(&v[i][12], sc));
+            if ((cseg & 1) == 0) a.e_row[(g * M + m) * eb_row + n0 / 32] = static_cast<uint8_t>(e);
+        }
+    }
+
+    if constexpr (COL) {
+        __shared__ uint32_t s_tr[128][128 / 4 + 1]; // transposed bytes, padded
+        const int64_t       eb_col = a.M_pad / 32;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float c = fmaxf(fmaxf(fabsf(v[0][j]), fabsf(v[1][j])), fmaxf(fabsf(v[2][j]), fabsf(v[3][j])));
+            if (!a.use2d_col) {
+                c = fmaxf(c, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0x128, 0xf, 0xf, false)));
+                c = fmaxf(c, __shfl_xor(c, 16));
+                c = fmaxf(c, __shfl_xor(c, 32));
+            } else {
+                c = blk;
+            }
+            const int   e  = mx_e8m0<FMT>(c);
+            const float sc = mx_qscale(e);
+            uint32_t    packed = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(v[i][j], sc))) << (8 * i);
+            s_tr[cseg * 16 + j][rgrp] = packed;
+            const int64_t n = n0 + j;
+            if ((rgrp & 7) == 0 && n < N) a.e_col[(g * N + n) * eb_col + tm * 4 + wave] = static_cast<uint8_t>(e);
+        }
         __syncthreads();
-    }
-    if (q_row != nullptr) {
-        // lane t: row t>>2, 16 cols; 32-col block = lanes pair (t, t^1)
-        const int     rl = t >> 2, cl = (t & 3) * 16;
-        const int64_t m  = m0 + rl;
-        float         v[16];
-        float         a = 0.0f;
-        for (int j = 0; j < 16; ++j) {
-            v[j] = s_tile[rl][cl + j];
-            a    = fmaxf(a, fabsf(v[j]));
-        }
-        a = fmaxf(a, dpp_f<PTA_DPP_QUAD_XOR1>(a));
-        if (use2d_row) a = s_bmax[rl >> 5][cl >> 5];
-        const int   e  = mx_e8m0<FMT>(a);
-        const float sc = mx_qscale(e);
-        if (m < M && n0 + cl < N_pad) {
-            uint8_t *dst = q_row + (g * M + m) * N_pad + n0 + cl;
-            *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(v, sc), quant4<FMT>(v + 4, sc),
-                                                         quant4<FMT>(v + 8, sc), quant4<FMT>(v + 12, sc));
-            if ((t & 1) == 0) e_row[(g * M + m) * (N_pad / 32) + (n0 + cl) / 32] = static_cast<uint8_t>(e);
-        }
-    }
-    if (q_col != nullptr) {
-        // lane t: column t>>2, 16 rows ((t&3)*16); 32-row block = lanes pair (t, t^1)
-        const int     cl = t >> 2, rl = (t & 3) * 16;
-        const int64_t n  = n0 + cl;
-        float         v[16];
-        float         a = 0.0f;
-        for (int j = 0; j < 16; ++j) {
-            v[j] = s_tile[rl + j][cl];
-            a    = fmaxf(a, fabsf(v[j]));
-        }
-        a = fmaxf(a, dpp_f<PTA_DPP_QUAD_XOR1>(a));
-        if (use2d_col) a = s_bmax[rl >> 5][cl >> 5];
-        const int   e  = mx_e8m0<FMT>(a);
-        const float sc = mx_qscale(e);
-        if (n < N && m0 + rl < M_pad) {
-            uint8_t *dst = q_col + (g * N + n) * M_pad + m0 + rl;
-            *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(v, sc), quant4<FMT>(v + 4, sc),
-                                                         quant4<FMT>(v + 8, sc), quant4<FMT>(v + 12, sc));
-            if ((t & 1) == 0) e_col[(g * N + n) * (M_pad / 32) + (m0 + rl) / 32] = static_cast<uint8_t>(e);
+        // 128 output rows (n) x 128 bytes (m) in 16-byte chunks
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int     c  = it * NT + t;
+            const int     nl = c >> 3;
+            const int     mc = (c & 7) * 16;
+            const int64_t n  = tn * 128 + nl;
+            if (n >= N) continue;
+            const uint32_t *src = &s_tr[nl][mc >> 2];
+            *reinterpret_cast<uint4 *>(a.q_col + (g * N + n) * a.M_pad + tm * 128 + mc) =
+                make_uint4(src[0], src[1], src[2], src[3]);
         }
     }
 }
@@ -532,10 +573,24 @@ int check_in(const void *x, int in_dtype, int fmt) {
 template <int IN_DT, int FMT>
 int mx_launch(const void *x, int64_t G, int64_t M, int64_t N, uint8_t *q_row, uint8_t *e_row,
               int u2r, uint8_t *q_col, uint8_t *e_col, int u2c, hipStream_t st) {
-    const int64_t M_pad = cdiv(M, 128) * 128, N_pad = cdiv(N, 128) * 128;
-    const dim3    grid(static_cast<uint32_t>(M_pad / 64), static_cast<uint32_t>(N_pad / 64),
-                       static_cast<uint32_t>(G));
-    mx_quant_kernel<IN_DT, FMT><<<grid, NT, 0, st>>>(x, M, N, M_pad, N_pad, q_row, e_row, u2r, q_col, e_col, u2c);
+    MXArgs a{};
+    a.x = x; a.M = M; a.N = N;
+    a.M_pad = cdiv(M, 128) * 128;
+    a.N_pad = cdiv(N, 128) * 128;
+    a.q_row = q_row; a.e_row = e_row; a.q_col = q_col; a.e_col = e_col;
+    a.use2d_row = u2r; a.use2d_col = u2c;
+    a.vec = aligned16(x) ? 1 : 0;
+    const dim3 grid(static_cast<uint32_t>(a.M_pad / 128), static_cast<uint32_t>(a.N_pad / 128),
+                    static_cast<uint32_t>(G));
+    // inputs beyond the MALL's reach are streamed with non-temporal loads
+    const bool stream = a.vec && G * M * N * InTraits<IN_DT>::bytes >= (192ll << 20);
+#define PTA_MX_GO(R, C)                                                                            \
+    if (stream) mx_tile_kernel<IN_DT, FMT, R, C, true><<<grid, NT, 0, st>>>(a);                    \
+    else mx_tile_kernel<IN_DT, FMT, R, C, false><<<grid, NT, 0, st>>>(a);
+    if (q_row && q_col) { PTA_MX_GO(true, true) }
+    else if (q_row) { PTA_MX_GO(true, false) }
+    else { PTA_MX_GO(false, true) }
+#undef PTA_MX_GO
     PTA_CHECK_LAUNCH();
     return PTA_OK;
 }
