@@ -197,11 +197,24 @@ __device__ __forceinline__ float max16(float v) {
     return v;
 }
 
+// max(v, v of lane ^ 16) and max(v, v of lane ^ 32) on the VALU: with both
+// operands equal, v_permlane16_swap leaves rows (r0, r0, r2, r2) in one result
+// and (r1, r1, r3, r3) in the other (rows of 16 lanes); v_permlane32_swap does
+// the same with the two halves of the wave.
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // max over the whole wave (result valid in every lane)
 __device__ __forceinline__ float max64(float v) {
     v = max16(v);
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
+    v = max_xor16(v);
+    v = max_xor32(v);
     return v;
 }
 

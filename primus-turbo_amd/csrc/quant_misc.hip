@@ -316,8 +316,7 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     }
     if (a.use2d_row || a.use2d_col) {
         blk = fmaxf(blk, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(blk), 0x128, 0xf, 0xf, false)));
-        blk = fmaxf(blk, __shfl_xor(blk, 16));
-        blk = fmaxf(blk, __shfl_xor(blk, 32));
+        blk = max_xor32(max_xor16(blk));
     }
 
     if constexpr (ROW) {
@@ -343,8 +342,7 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             float c = fmaxf(fmaxf(fabsf(v[0][j]), fabsf(v[1][j])), fmaxf(fabsf(v[2][j]), fabsf(v[3][j])));
             if (!a.use2d_col) {
                 c = fmaxf(c, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0x128, 0xf, 0xf, false)));
-                c = fmaxf(c, __shfl_xor(c, 16));
-                c = fmaxf(c, __shfl_xor(c, 32));
+                c = max_xor32(max_xor16(c));
             } else {
                 c = blk;
             }
