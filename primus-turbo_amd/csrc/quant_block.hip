@@ -91,27 +91,69 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     const char *xb = reinterpret_cast<const char *>(args.x) +
                      batch * args.batch_stride_x * InTraits<IN_DT>::bytes;
 
-    float v[4][16];
+    // The lane's 4 x 16 inputs stay packed (8 VGPRs per row for 16-bit types)
+    // and are widened to fp32 at each use: the kernel then fits in few enough
+    // VGPRs that every tile of a large tensor has its loads in flight at once.
+    constexpr int CH = InTraits<IN_DT>::bytes; // 16-byte chunks per 16 elements
+    uint4 raw[4][CH];
     bool  rvalid[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t r = row_base + rgrp * 4 + i;
         rvalid[i]       = (r >= row_lo) && (r < row_hi);
-        if (VEC && rvalid[i] && n0 + 16 <= N) {
-            float a[8], b[8];
-            load8<IN_DT, STREAM>(xb, r * N + n0, a);
-            load8<IN_DT, STREAM>(xb, r * N + n0 + 8, b);
+        if (VEC) {
+            typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+            const bool   ok = rvalid[i] && n0 + 16 <= N;
+            const v4u   *p  = reinterpret_cast<const v4u *>(xb + (r * N + n0) * InTraits<IN_DT>::bytes);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                v[i][j]     = a[j];
-                v[i][j + 8] = b[j];
+            for (int c = 0; c < CH; ++c) {
+                v4u w = v4u{0u, 0u, 0u, 0u};
+                if (ok) {
+                    if constexpr (STREAM) w = __builtin_nontemporal_load(p + c);
+                    else w = p[c];
+                }
+                raw[i][c] = make_uint4(w.x, w.y, w.z, w.w);
             }
         } else {
+            // scalar path: widen then re-pack into the raw layout
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                v[i][j] = (rvalid[i] && n0 + j < N) ? load_scalar<IN_DT>(xb, r * N + n0 + j) : 0.0f;
+            for (int c = 0; c < CH; ++c) {
+                uint32_t wd[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if constexpr (IN_DT == PTA_F32) {
+                        const int j = 4 * c + k;
+                        wd[k] = (rvalid[i] && n0 + j < N) ? __float_as_uint(load_scalar<IN_DT>(xb, r * N + n0 + j)) : 0u;
+                    } else {
+                        const int  j0 = 8 * c + 2 * k;
+                        const auto rd = [&](int j) -> uint32_t {
+                            return (rvalid[i] && n0 + j < N) ? reinterpret_cast<const uint16_t *>(xb)[r * N + n0 + j] : 0u;
+                        };
+                        wd[k] = rd(j0) | (rd(j0 + 1) << 16);
+                    }
+                }
+                raw[i][c] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+            }
         }
     }
+    // element (i, j) of the lane's 4 x 16 block as fp32
+    auto V = [&](int i, int j) -> float {
+        if constexpr (IN_DT == PTA_F32) {
+            const uint4    w  = raw[i][j >> 2];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+            return __uint_as_float(ws[j & 3]);
+        } else {
+            const uint4    w  = raw[i][j >> 3];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+            const uint32_t d  = ws[(j >> 1) & 3];
+            if constexpr (IN_DT == PTA_BF16) return __uint_as_float((j & 1) ? (d & 0xffff0000u) : (d << 16));
+            else return f16_bits_to_f32((j & 1) ? (d >> 16) : (d & 0xffffu));
+        }
+    };
+    auto Q4 = [&](int i, int j, float sc) -> uint32_t {
+        return cvt4_fp8<FMT>(qclamp<FMT>(V(i, j), sc), qclamp<FMT>(V(i, j + 1), sc), qclamp<FMT>(V(i, j + 2), sc),
+                             qclamp<FMT>(V(i, j + 3), sc));
+    };
 
     __shared__ float s_part[16][TILE]; // col partial maxima (16 lane-rows x 128 cols)
     __shared__ float s_cscale[TILE];
@@ -125,7 +167,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         for (int i = 0; i < 4; ++i) {
             float a = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[i][j]));
+            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(V(i, j)));
             a                = max8(a);
             const float sc   = scale_from_amax<FMT>(a, 1e-4f);
             const float sinv = 1.0f / sc;
@@ -133,7 +175,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             if (rvalid[i]) {
                 uint32_t w[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) w[k] = quant4<FMT>(&v[i][4 * k], sc);
+                for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc);
                 uint8_t *dst = args.q_row + r * N + n0;
                 if (VEC && n0 + 16 <= N) {
                     *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
@@ -155,7 +197,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         float ca[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            float a = fmaxf(fmaxf(fabsf(v[0][j]), fabsf(v[1][j])), fmaxf(fabsf(v[2][j]), fabsf(v[3][j])));
+            float a = fmaxf(fmaxf(fabsf(V(0, j)), fabsf(V(1, j))), fmaxf(fabsf(V(2, j)), fabsf(V(3, j))));
             // lanes l and l^8 share a column segment inside each 16-lane row
             a     = fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x128, 0xf, 0xf, false)));
             ca[j] = a;
@@ -191,8 +233,8 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 uint32_t w[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    w[k] = cvt4_fp8<FMT>(qclamp<FMT>(v[i][4 * k], cs[4 * k]), qclamp<FMT>(v[i][4 * k + 1], cs[4 * k + 1]),
-                                         qclamp<FMT>(v[i][4 * k + 2], cs[4 * k + 2]), qclamp<FMT>(v[i][4 * k + 3], cs[4 * k + 3]));
+                    w[k] = cvt4_fp8<FMT>(qclamp<FMT>(V(i, 4 * k), cs[4 * k]), qclamp<FMT>(V(i, 4 * k + 1), cs[4 * k + 1]),
+                                         qclamp<FMT>(V(i, 4 * k + 2), cs[4 * k + 2]), qclamp<FMT>(V(i, 4 * k + 3), cs[4 * k + 3]));
                 uint8_t *dst = args.q_col + prow * N + n0;
                 if (VEC && n0 + 16 <= N) {
                     *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
@@ -209,7 +251,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 uint32_t packed = 0;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(v[i][j], cs[j]))) << (8 * i);
+                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(V(i, j), cs[j]))) << (8 * i);
                 s_tr[cseg * 16 + j][rgrp] = packed;
             }
             __syncthreads();
@@ -236,7 +278,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[i][j]));
+            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(V(i, j)));
         a = max64(a);
         if (lane == 0) s_wmax[wave] = a;
         __syncthreads();
@@ -250,7 +292,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             const int64_t r = row_base + rgrp * 4 + i;
             uint32_t      w[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) w[k] = quant4<FMT>(&v[i][4 * k], sc);
+            for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc);
             if (!rvalid[i]) continue;
             uint8_t *dst = qb + r * N + n0;
             if (VEC && n0 + 16 <= N) {
@@ -268,7 +310,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 uint32_t packed = 0;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(v[i][j], sc))) << (8 * i);
+                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(V(i, j), sc))) << (8 * i);
                 s_tr[cseg * 16 + j][rgrp] = packed;
             }
             __syncthreads();
