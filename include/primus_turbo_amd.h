@@ -130,6 +130,25 @@ int pta_quantize_mxfp8(const void *x, int in_dtype, int64_t G, int64_t M, int64_
                        uint8_t *e_row, int use_2d_row, void *q_col, uint8_t *e_col, int use_2d_col,
                        int fmt, pta_stream_t stream);
 
+/* Grouped MXFP8 (block 32, E8M0) of x[M, N] whose rows are split into G
+ * groups by group_offs[G+1] (device).  Each group is zero-padded along M to
+ * 32 rows for the rowwise output and to 128 for the colwise output; the padded
+ * lengths and offsets are written to lens_row / offs_row (32) and lens_col /
+ * offs_col (128) on the device.  Rowwise: q_row[M_pad_row, N_pad] with group
+ * g at rows offs_row[g] .. offs_row[g+1], e_row[M_pad_row, N_pad/32],
+ * M_pad_row = roundup(M + 32 G, 32).  Colwise (transposed): q_col[N, M_pad_col]
+ * with group g at columns offs_col[g] .., e_col[N, M_pad_col/32],
+ * M_pad_col = roundup(M + 128 G, 128).  Padding inside a group's padded range
+ * is zero (bytes and exponents); rows / columns past the last group are not
+ * written.  Either output pair may be NULL; 2-D exponent blocks are rejected.
+ * Replaces grouped_quantize_mxfp8 / grouped_quantize_mxfp8_dual
+ * (csrc/pytorch/quantization/quantization.cpp:969-1195). */
+int pta_grouped_quantize_mxfp8(const void *x, int in_dtype, int64_t M, int64_t N, int64_t G,
+                               const int64_t *group_lens, const int64_t *group_offs, void *q_row,
+                               uint8_t *e_row, int use_2d_row, int64_t *lens_row, int64_t *offs_row,
+                               void *q_col, uint8_t *e_col, int use_2d_col, int64_t *lens_col,
+                               int64_t *offs_col, int fmt, pta_stream_t stream);
+
 /* ============================================================================
  * Dequantization: y = out_dtype(float(q) * scale_inv)
  * ========================================================================== */
@@ -167,6 +186,12 @@ int pta_transpose_u8(const void *x, int64_t B, int64_t M, int64_t N, void *y, pt
 /* offs[0] = 0, offs[i+1] = offs[i] + lens[i] (int64, device).
  * Replaces grouped_gemm_compute_offs (csrc/pytorch/grouped_gemm/ck_grouped_gemm.cpp:63-80). */
 int pta_grouped_compute_offs(const int64_t *lens, int64_t *offs, int64_t G, pta_stream_t stream);
+
+/* lens_padded[g] = roundup(lens[g], align) (skipped when NULL), offs_padded =
+ * their exclusive prefix sum [G+1] (int64, device).  Replaces
+ * compute_padded_layout_gpu (called at csrc/pytorch/quantization/quantization.cpp:1047). */
+int pta_grouped_compute_padded_layout(const int64_t *lens, int64_t *lens_padded, int64_t *offs_padded,
+                                      int64_t G, int64_t align, pta_stream_t stream);
 
 /* padded_offs[0] = 0, padded_offs[g+1] = padded_offs[g] + roundup(offs[g+1] - offs[g], align)
  * (int64, device).  Replaces the padded-offset computation of
@@ -219,7 +244,13 @@ int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b
 /* Grouped GEMM over G groups of rows of A (M-grouped, forward / dgrad):
  * out[offs[g]:offs[g+1]] = A[offs[g]:offs[g+1]] @ op(B[g]), B[G, N, K]
  * (trans_b = 1) or [G, K, N].  group_offs[G+1] on device, never read by the host.
- * Rows [group_offs[G], M_total) of out are set to 0.
+ * group_offs_out (may be NULL): when set, A's rows follow the padded layout
+ * group_offs and group g's output rows are written packed at
+ * out[group_offs_out[g] : group_offs_out[g+1]] (only that many rows of the
+ * group are computed into out) -- the MX grouped forward reads 32-padded rows
+ * this way (ops/grouped_gemm_fp8.py:692-707 of the reference).
+ * Rows [offs_out[G], M_total) of out are set to 0 (offs_out = group_offs_out
+ * or group_offs).
  * Blockwise: a_scale transposed [K/128, M_total], b_scale[G, N/128, K/128]
  * (trans_b = 1) or [G, K/128, N/128].  Tensorwise: device scalars.
  * Rowwise: a_scale[M_total], b_scale[G, N].
@@ -228,10 +259,10 @@ int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b
 size_t pta_grouped_gemm_fp8_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G,
                                            int trans_b, int granularity);
 int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scale, const void *b, int b_fmt,
-                         const void *b_scale, int trans_b, const int64_t *group_offs, int64_t G,
-                         int64_t M_total, int64_t N, int64_t K, void *out, int c_dtype,
-                         int granularity, int num_cu, void *workspace, size_t workspace_bytes,
-                         pta_stream_t stream);
+                         const void *b_scale, int trans_b, const int64_t *group_offs,
+                         const int64_t *group_offs_out, int64_t G, int64_t M_total, int64_t N,
+                         int64_t K, void *out, int c_dtype, int granularity, int num_cu,
+                         void *workspace, size_t workspace_bytes, pta_stream_t stream);
 
 /* Variable-K grouped GEMM (wgrad): for each g,
  * out[g] = op_c( lhs[seg_g]^T @ rhs[seg_g] ) with seg_g = rows
@@ -249,6 +280,20 @@ int pta_grouped_gemm_fp8_variable_k(const void *lhs, int lhs_fmt, const void *lh
                                     int64_t OUT_M, int64_t OUT_N, void *out, int c_dtype,
                                     int trans_c, int granularity, int num_cu, void *workspace,
                                     size_t workspace_bytes, pta_stream_t stream);
+
+/* Variable-K grouped GEMM on operands already transposed and padded per
+ * group (MX wgrad): out[g] = op_c( lhs_t[:, seg_g] @ rhs_t[:, seg_g]^T ) with
+ * lhs_t[OUT_M, K_pad], rhs_t[OUT_N, K_pad], seg_g = columns
+ * [group_offs[g], group_offs[g+1]) (multiples of 128), E8M0 scales
+ * lhs_scale[OUT_M, K_pad/32], rhs_scale[OUT_N, K_pad/32]; out[G, OUT_M, OUT_N]
+ * (trans_c = 0) or [G, OUT_N, OUT_M].  Empty groups give zero slices.
+ * Replaces the MX call of grouped_gemm_fp8_variable_k_impl
+ * (primus_turbo/pytorch/ops/grouped_gemm_fp8.py:760-775). */
+int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt, const void *lhs_scale,
+                                       const void *rhs_t, int rhs_fmt, const void *rhs_scale,
+                                       const int64_t *group_offs, int64_t G, int64_t K_pad,
+                                       int64_t OUT_M, int64_t OUT_N, void *out, int c_dtype,
+                                       int trans_c, int granularity, pta_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -216,6 +216,10 @@ def quant_block_segment(x, fmt, group_lens, block=128):
 def quant_mx(x, fmt, direction, use_2d=False):
     """direction 1 = rowwise, 0 = colwise (transposed output).  x is [M,N] or [G,M,N]."""
     raw, dt = _as_raw(x)
+    return _quant_mx_raw(raw, dt, fmt, direction, use_2d)
+
+
+def _quant_mx_raw(raw, dt, fmt, direction, use_2d=False):
     batched = raw.ndim == 3
     r3 = raw if batched else raw[None]
     G, M, N = r3.shape
@@ -231,6 +235,45 @@ def quant_mx(x, fmt, direction, use_2d=False):
         q = q.reshape(G, -1, q.shape[-1])
         e = e.reshape(G, -1, e.shape[-1])
     return q, e
+
+
+def quant_mx_grouped(x, fmt, group_lens):
+    """Grouped MXFP8 of x[M, N] (rows split by group_lens): each group is
+    zero-padded along M to 32 rows (rowwise output) and to 128 (colwise,
+    transposed), the layout of grouped_quantize_mxfp8(_dual) in the reference
+    (csrc/pytorch/quantization/quantization.cpp:969-1195).  Composed from
+    quant_mx on each padded group, so each block sees exactly the rows of one
+    group plus zeros.  Returns (q_row [Mr, Np], e_row, offs_row, q_col [N, Mc],
+    e_col, offs_col) with rows / columns outside every group left at 0."""
+    raw, dt = _as_raw(x)
+    M, N = raw.shape
+    lens = [int(v) for v in group_lens]
+    G = len(lens)
+    Mr = -(-(M + 32 * G) // 32) * 32
+    Mc = -(-(M + 128 * G) // 128) * 128
+    Np = -(-N // 128) * 128
+    q_row = np.zeros((Mr, Np), np.uint8)
+    e_row = np.zeros((Mr, Np // 32), np.uint8)
+    q_col = np.zeros((N, Mc), np.uint8)
+    e_col = np.zeros((N, Mc // 32), np.uint8)
+    offs_row, offs_col = [0], [0]
+    s = 0
+    for L in lens:
+        pr, pc = -(-L // 32) * 32, -(-L // 128) * 128
+        if L:
+            seg = raw[s:s + L]
+            pad_c = np.zeros((pc, N), raw.dtype)
+            pad_c[:L] = seg
+            qr, er = _quant_mx_raw(np.ascontiguousarray(pad_c[:pr]), dt, fmt, 1)
+            qc, ec = _quant_mx_raw(pad_c, dt, fmt, 0)
+            q_row[offs_row[-1]:offs_row[-1] + pr] = qr[:, :Np]
+            e_row[offs_row[-1]:offs_row[-1] + pr] = er
+            q_col[:, offs_col[-1]:offs_col[-1] + pc] = qc[:, :pc]
+            e_col[:, offs_col[-1] // 32:(offs_col[-1] + pc) // 32] = ec[:, :pc // 32]
+        offs_row.append(offs_row[-1] + pr)
+        offs_col.append(offs_col[-1] + pc)
+        s += L
+    return q_row, e_row, np.array(offs_row, np.int64), q_col, e_col, np.array(offs_col, np.int64)
 
 
 def mx_e8m0(amax: float, fmt: int) -> int:

@@ -81,6 +81,9 @@ struct GemmArgs {
     // nothing else indexed by group).  group_offs stays on the device.
     int            group_mode;
     const int64_t *group_offs;
+    const int64_t *group_offs_out; // group_mode 1: C rows of group g start at group_offs_out[g]
+                                   // and number group_offs_out[g+1] - group_offs_out[g] (NULL:
+                                   // same rows as A)
     int64_t        G;
     int64_t        b_gstride, sb_gstride, c_gstride; // elements / bytes per group
 };
@@ -216,6 +219,15 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
         if (grp < 0) return; // past the last tile (grid is an upper bound)
         m0 = gstart + (mt - cum) * BM;
         M  = gend; // rows [m0, gend) are valid
+        if (g.group_offs_out != nullptr) {
+            // A rows are a padded layout; only the group's true rows are written,
+            // packed at group_offs_out[grp]
+            constexpr int64_t ob = OUT_DT == PTA_F32 ? 4 : 2;
+            const int64_t     o0 = g.group_offs_out[grp], o1 = g.group_offs_out[grp + 1];
+            M = min<int64_t>(gend, gstart + (o1 - o0));
+            C = reinterpret_cast<uint8_t *>(g.c) + (o0 - gstart) * g.ldc * ob;
+            if (m0 >= M) return;
+        }
         n0 = tn * BN_;
         B  = g.b + grp * g.b_gstride;
         SB = reinterpret_cast<const uint8_t *>(g.sb) + grp * g.sb_gstride;

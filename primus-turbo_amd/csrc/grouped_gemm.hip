@@ -104,9 +104,10 @@ extern "C" size_t pta_grouped_gemm_fp8_workspace_size(int64_t /*M_total*/, int64
 
 extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scale, const void *b,
                                     int b_fmt, const void *b_scale, int trans_b,
-                                    const int64_t *group_offs, int64_t G, int64_t M_total, int64_t N,
-                                    int64_t K, void *out, int c_dtype, int granularity, int num_cu,
-                                    void *workspace, size_t workspace_bytes, pta_stream_t stream) {
+                                    const int64_t *group_offs, const int64_t *group_offs_out, int64_t G,
+                                    int64_t M_total, int64_t N, int64_t K, void *out, int c_dtype,
+                                    int granularity, int num_cu, void *workspace, size_t workspace_bytes,
+                                    pta_stream_t stream) {
     clear_error();
     (void)num_cu;
     const int sm = gran_sm(granularity);
@@ -131,7 +132,7 @@ extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scal
     g.a = static_cast<const uint8_t *>(a); g.b = bp; g.c = out;
     g.M = M_total; g.N = N; g.K = K; g.lda = K; g.ldb = K; g.ldc = N;
     g.sa = a_scale; g.sb = b_scale;
-    g.group_mode = 1; g.group_offs = group_offs; g.G = G;
+    g.group_mode = 1; g.group_offs = group_offs; g.group_offs_out = group_offs_out; g.G = G;
     g.b_gstride = N * K;
     g.aligned_c = ((N * static_cast<int64_t>(eb)) % 16 == 0) && aligned16(out);
     g.group_m = 1;
@@ -156,8 +157,8 @@ extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scal
     g.tiles_n = static_cast<int>(cdiv(N, BN));
     g.tiles_m = static_cast<int>(cdiv(M_total, BM) + G);
     if (int rc = run(g, sm, false, b2d, a_fmt, b_fmt, c_dtype, st)) return rc;
-    zero_tail_kernel<<<64, 256, 0, st>>>(group_offs, G, M_total, N * static_cast<int64_t>(eb),
-                                         static_cast<uint8_t *>(out));
+    zero_tail_kernel<<<64, 256, 0, st>>>(group_offs_out ? group_offs_out : group_offs, G, M_total,
+                                         N * static_cast<int64_t>(eb), static_cast<uint8_t *>(out));
     PTA_CHECK_LAUNCH();
     return PTA_OK;
 }
@@ -229,6 +230,44 @@ extern "C" int pta_grouped_gemm_fp8_variable_k(const void *lhs, int lhs_fmt, con
     } else {
         g.sa_bytes = 4; g.sb_bytes = 4;
     }
+    const int fa = swap ? rhs_fmt : lhs_fmt, fb = swap ? lhs_fmt : rhs_fmt;
+    return run(g, sm, false, false, fa, fb, c_dtype, st);
+}
+
+extern "C" int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt, const void *lhs_scale,
+                                                  const void *rhs_t, int rhs_fmt, const void *rhs_scale,
+                                                  const int64_t *group_offs, int64_t G, int64_t K_pad,
+                                                  int64_t OUT_M, int64_t OUT_N, void *out, int c_dtype,
+                                                  int trans_c, int granularity, pta_stream_t stream) {
+    clear_error();
+    const int sm = gran_sm(granularity);
+    PTA_CHECK_ARG(sm == SM_MX, "the pre-transposed variable-K entry supports MX_BLOCKWISE");
+    PTA_CHECK_ARG(lhs_t && rhs_t && out && lhs_scale && rhs_scale && group_offs, "NULL pointer argument");
+    PTA_CHECK_ARG(G >= 1 && G <= 65535 && K_pad >= 0 && OUT_M >= 0 && OUT_N >= 0, "bad shape");
+    PTA_CHECK_ARG(K_pad % 128 == 0, "K_pad must be a multiple of 128");
+    PTA_CHECK_ARG(c_dtype == PTA_BF16 || c_dtype == PTA_F16 || c_dtype == PTA_F32, "unsupported output dtype");
+    PTA_CHECK_ARG(aligned16(lhs_t) && aligned16(rhs_t), "operands must be 16-byte aligned");
+    if (OUT_M == 0 || OUT_N == 0) return PTA_OK;
+    hipStream_t  st = as_stream(stream);
+    const size_t eb = c_dtype == PTA_F32 ? 4 : 2;
+    // NT problem per group: C[m, n] = sum_{k in segment g} lhs_t[m, k] rhs_t[n, k];
+    // segment offsets are multiples of 128, so the exponent index of K block
+    // kb is 4 * kb + (0..3) in the padded layout
+    GemmArgs   g{};
+    const bool swap = trans_c != 0;
+    g.a = static_cast<const uint8_t *>(swap ? rhs_t : lhs_t);
+    g.b = static_cast<const uint8_t *>(swap ? lhs_t : rhs_t);
+    g.M = swap ? OUT_N : OUT_M; g.N = swap ? OUT_M : OUT_N; g.K = K_pad;
+    g.lda = K_pad; g.ldb = K_pad; g.ldc = g.N;
+    g.sa = swap ? rhs_scale : lhs_scale; g.sb = swap ? lhs_scale : rhs_scale;
+    g.sa_m = K_pad / 32; g.sb_m = K_pad / 32;
+    g.sa_bytes = g.M * (K_pad / 32); g.sb_bytes = g.N * (K_pad / 32);
+    g.group_mode = 2; g.group_offs = group_offs; g.G = G;
+    g.c = out; g.c_gstride = OUT_M * OUT_N * static_cast<int64_t>(eb);
+    g.aligned_c = ((g.N * static_cast<int64_t>(eb)) % 16 == 0) && aligned16(out);
+    g.group_m = 4;
+    g.tiles_m = static_cast<int>(cdiv(g.M, BM));
+    g.tiles_n = static_cast<int>(cdiv(g.N, BN));
     const int fa = swap ? rhs_fmt : lhs_fmt, fb = swap ? lhs_fmt : rhs_fmt;
     return run(g, sm, false, false, fa, fb, c_dtype, st);
 }

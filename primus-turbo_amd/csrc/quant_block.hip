@@ -548,6 +548,16 @@ extern "C" int pta_grouped_compute_padded_offs(const int64_t *offs, int64_t *pad
     return PTA_OK;
 }
 
+extern "C" int pta_grouped_compute_padded_layout(const int64_t *lens, int64_t *lens_padded,
+                                                 int64_t *offs_padded, int64_t G, int64_t align,
+                                                 pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(lens && offs_padded && G >= 0 && align >= 1, "bad arguments");
+    padded_offs_kernel<<<1, 256, 0, as_stream(stream)>>>(lens, lens_padded, offs_padded, G, align);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
 extern "C" int pta_grouped_compute_offs(const int64_t *lens, int64_t *offs, int64_t G,
                                         pta_stream_t stream) {
     clear_error();

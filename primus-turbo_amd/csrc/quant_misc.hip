@@ -267,9 +267,13 @@ struct MXArgs {
     int64_t     M, N, M_pad, N_pad;
     uint8_t    *q_row, *e_row, *q_col, *e_col;
     int         use2d_row, use2d_col, vec;
+    // grouped rows (x[M, N] split by goffs[G+1]): tiles live in the 128-padded
+    // colwise space offs_col; the rowwise output places group g at offs_row[g]
+    const int64_t *goffs, *offs_row, *offs_col;
+    int64_t        G;
 };
 
-template <int IN_DT, int FMT, bool ROW, bool COL, bool STREAM>
+template <int IN_DT, int FMT, bool ROW, bool COL, bool STREAM, bool GROUPED>
 __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     const int     t    = threadIdx.x;
     const int     wave = t >> 6;
@@ -280,11 +284,36 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     const int64_t n0 = tn * 128 + cseg * 16;
     const char   *xb = reinterpret_cast<const char *>(a.x) + g * M * N * InTraits<IN_DT>::bytes;
 
+    // local row lr of this tile: x row xr0 + lr if lr < nval, rowwise output
+    // row orow0 + lr if lr < nout (rows nval .. nout - 1 are zero padding)
+    int64_t xr0, nval, orow0, nout;
+    if constexpr (GROUPED) {
+        const int64_t pad0 = tm * 128;
+        if (pad0 >= a.offs_col[a.G]) return;
+        int64_t lo = 0, hi = a.G - 1; // last group whose padded range starts at or before pad0
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if (a.offs_col[mid] <= pad0) lo = mid;
+            else hi = mid - 1;
+        }
+        const int64_t li0 = pad0 - a.offs_col[lo];
+        const int64_t len = a.goffs[lo + 1] - a.goffs[lo];
+        xr0   = a.goffs[lo] + li0;
+        nval  = len - li0;
+        orow0 = a.offs_row[lo] + li0;
+        nout  = (len + 31) / 32 * 32 - li0;
+    } else {
+        xr0   = tm * 128;
+        nval  = M - tm * 128;
+        orow0 = g * M + tm * 128;
+        nout  = nval;
+    }
+
     float v[4][16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int64_t m  = tm * 128 + rgrp * 4 + i;
-        const bool    ok = m < M && n0 < N; // N % 32 == 0: a lane's 16 columns are all in or all out
+        const int64_t m  = xr0 + rgrp * 4 + i;
+        const bool    ok = rgrp * 4 + i < nval && n0 < N; // N % 32 == 0: all 16 columns in or out
         if (a.vec) {
             float lo[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             if (ok) {
@@ -323,14 +352,15 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         const int64_t eb_row = a.N_pad / 32;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int64_t m = tm * 128 + rgrp * 4 + i;
-            if (m >= M) continue;
-            const int   e  = mx_e8m0<FMT>(a.use2d_row ? blk : ra[i]);
-            const float sc = mx_qscale(e);
-            uint8_t    *dst = a.q_row + (g * M + m) * a.N_pad + n0;
+            const int lr = rgrp * 4 + i;
+            if (lr >= nout) continue;
+            const int64_t orow = orow0 + lr;
+            const int     e    = mx_e8m0<FMT>(a.use2d_row ? blk : ra[i]);
+            const float   sc   = mx_qscale(e);
+            uint8_t      *dst  = a.q_row + orow * a.N_pad + n0;
             *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(&v[i][0], sc), quant4<FMT>(&v[i][4], sc),
                                                          quant4<FMT>(&v[i][8], sc), quant4<FMT>(&v[i][12], sc));
-            if ((cseg & 1) == 0) a.e_row[(g * M + m) * eb_row + n0 / 32] = static_cast<uint8_t>(e);
+            if ((cseg & 1) == 0) a.e_row[orow * eb_row + n0 / 32] = static_cast<uint8_t>(e);
         }
     }
 
@@ -583,8 +613,33 @@ int mx_launch(const void *x, int64_t G, int64_t M, int64_t N, uint8_t *q_row, ui
     // inputs beyond the MALL's reach are streamed with non-temporal loads
     const bool stream = a.vec && G * M * N * InTraits<IN_DT>::bytes >= (192ll << 20);
 #define PTA_MX_GO(R, C)                                                                            \
-    if (stream) mx_tile_kernel<IN_DT, FMT, R, C, true><<<grid, NT, 0, st>>>(a);                    \
-    else mx_tile_kernel<IN_DT, FMT, R, C, false><<<grid, NT, 0, st>>>(a);
+    if (stream) mx_tile_kernel<IN_DT, FMT, R, C, true, false><<<grid, NT, 0, st>>>(a);             \
+    else mx_tile_kernel<IN_DT, FMT, R, C, false, false><<<grid, NT, 0, st>>>(a);
+    if (q_row && q_col) { PTA_MX_GO(true, true) }
+    else if (q_row) { PTA_MX_GO(true, false) }
+    else { PTA_MX_GO(false, true) }
+#undef PTA_MX_GO
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
+template <int IN_DT, int FMT>
+int mx_grouped_launch(const void *x, int64_t M, int64_t N, int64_t G, const int64_t *goffs,
+                      const int64_t *offs_row, const int64_t *offs_col, uint8_t *q_row, uint8_t *e_row,
+                      uint8_t *q_col, uint8_t *e_col, int u2r, int u2c, hipStream_t st) {
+    MXArgs a{};
+    a.x = x; a.M = M; a.N = N;
+    a.M_pad = cdiv(M + G * 128, 128) * 128; // colwise output columns
+    a.N_pad = cdiv(N, 128) * 128;
+    a.q_row = q_row; a.e_row = e_row; a.q_col = q_col; a.e_col = e_col;
+    a.use2d_row = u2r; a.use2d_col = u2c;
+    a.vec = aligned16(x) ? 1 : 0;
+    a.goffs = goffs; a.offs_row = offs_row; a.offs_col = offs_col; a.G = G;
+    const dim3 grid(static_cast<uint32_t>(a.M_pad / 128), static_cast<uint32_t>(a.N_pad / 128), 1);
+    const bool stream = a.vec && M * N * InTraits<IN_DT>::bytes >= (192ll << 20);
+#define PTA_MX_GO(R, C)                                                                            \
+    if (stream) mx_tile_kernel<IN_DT, FMT, R, C, true, true><<<grid, NT, 0, st>>>(a);              \
+    else mx_tile_kernel<IN_DT, FMT, R, C, false, true><<<grid, NT, 0, st>>>(a);
     if (q_row && q_col) { PTA_MX_GO(true, true) }
     else if (q_row) { PTA_MX_GO(true, false) }
     else { PTA_MX_GO(false, true) }
@@ -659,6 +714,32 @@ extern "C" int pta_quantize_mxfp8(const void *x, int in_dtype, int64_t G, int64_
     return PTA_DISPATCH_IN_FMT(in_dtype, fmt, mx_launch, x, G, M, N, static_cast<uint8_t *>(q_row),
                                e_row, use_2d_row, static_cast<uint8_t *>(q_col), e_col, use_2d_col,
                                as_stream(stream));
+}
+
+extern "C" int pta_grouped_quantize_mxfp8(const void *x, int in_dtype, int64_t M, int64_t N, int64_t G,
+                                          const int64_t *group_lens, const int64_t *group_offs,
+                                          void *q_row, uint8_t *e_row, int use_2d_row, int64_t *lens_row,
+                                          int64_t *offs_row, void *q_col, uint8_t *e_col, int use_2d_col,
+                                          int64_t *lens_col, int64_t *offs_col, int fmt,
+                                          pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_in(x, in_dtype, fmt)) return rc;
+    PTA_CHECK_ARG(in_dtype != PTA_F32, "MXFP8 quantization takes bf16 or fp16 input");
+    PTA_CHECK_ARG(G >= 1 && M >= 0 && N >= 0, "bad shape");
+    PTA_CHECK_ARG(N % 32 == 0, "N must be divisible by 32");
+    PTA_CHECK_ARG(group_lens && group_offs && lens_row && offs_row && lens_col && offs_col,
+                  "group arrays must be set");
+    PTA_CHECK_ARG((q_row == nullptr) == (e_row == nullptr), "q_row/e_row must both be set or NULL");
+    PTA_CHECK_ARG((q_col == nullptr) == (e_col == nullptr), "q_col/e_col must both be set or NULL");
+    PTA_CHECK_ARG(q_row || q_col, "no output requested");
+    PTA_CHECK_ARG((!q_row || aligned16(q_row)) && (!q_col || aligned16(q_col)), "outputs must be 16-byte aligned");
+    PTA_CHECK_ARG(!use_2d_row && !use_2d_col, "2-D exponent blocks are not supported for grouped rows");
+    if (int rc = pta_grouped_compute_padded_layout(group_lens, lens_row, offs_row, G, 32, stream)) return rc;
+    if (int rc = pta_grouped_compute_padded_layout(group_lens, lens_col, offs_col, G, 128, stream)) return rc;
+    if (M == 0 || N == 0) return PTA_OK;
+    return PTA_DISPATCH_IN_FMT(in_dtype, fmt, mx_grouped_launch, x, M, N, G, group_offs, offs_row, offs_col,
+                               static_cast<uint8_t *>(q_row), e_row, static_cast<uint8_t *>(q_col), e_col,
+                               use_2d_row, use_2d_col, as_stream(stream));
 }
 
 extern "C" int pta_dequantize_fp8_tensorwise(const void *q, int fmt, int64_t n, const float *scale_inv,

@@ -56,8 +56,17 @@ SIGNATURES = {
     "pta_grouped_gemm_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32]),
     "pta_grouped_gemm_fp8": (
         _i32,
-        [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _vp, _sz, _vp],
+        [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _vp, _sz, _vp],
     ),
+    "pta_grouped_gemm_fp8_variable_k_nt": (
+        _i32,
+        [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _vp],
+    ),
+    "pta_grouped_quantize_mxfp8": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp],
+    ),
+    "pta_grouped_compute_padded_layout": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "pta_grouped_gemm_fp8_variable_k_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
     "pta_grouped_gemm_fp8_variable_k": (
         _i32,

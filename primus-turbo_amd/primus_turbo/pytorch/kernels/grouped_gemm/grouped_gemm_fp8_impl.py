@@ -41,13 +41,17 @@ def grouped_gemm_fp8_impl(
 ) -> torch.Tensor:
     """out[offs[g]:offs[g+1]] = a[offs[g]:offs[g+1]] @ op(b[g]); rows past offs[G] are zero.
 
+    With ``group_offs_out`` the rows of ``a`` follow the padded layout
+    ``group_offs`` and group g's output rows are packed at
+    ``out[group_offs_out[g]:group_offs_out[g+1]]`` (the MX grouped forward;
+    ``out`` keeps a's row count and the caller slices the packed rows).
+
     a [M_total, K]; b [G, N, K] (trans_b) or [G, K, N].  Blockwise: a_scales
     transposed [K/128, M_total], b_scales [G, N/128, K/128] (trans_b) or
     [G, K/128, N/128].  Rowwise: a_scales [M_total(, 1)], b_scales [G, N(, 1)].
     Tensorwise: scalars.
     """
     assert not trans_a, "trans_a is not supported"
-    assert group_offs_out is None, "group_offs_out (MX grouped layout) is not supported"
     gran = _gran_code(granularity)
     a = a.contiguous()
     b = b.contiguous()
@@ -60,9 +64,11 @@ def grouped_gemm_fp8_impl(
         _C.query("pta_grouped_gemm_fp8_workspace_size", M_total, N, K, G, int(trans_b), gran), a.device
     )
     offs = group_offs.to(torch.int64).contiguous()
+    offs_out = None if group_offs_out is None else group_offs_out.to(torch.int64).contiguous()
     _C.call(
         "pta_grouped_gemm_fp8", _C.ptr(a), _C.fp8_code(a.dtype), _C.ptr(_scale(a_scales, gran)), _C.ptr(b),
-        _C.fp8_code(b.dtype), _C.ptr(_scale(b_scales, gran)), int(trans_b), _C.ptr(offs), G, M_total, N, K,
+        _C.fp8_code(b.dtype), _C.ptr(_scale(b_scales, gran)), int(trans_b), _C.ptr(offs), _C.ptr(offs_out), G,
+        M_total, N, K,
         _C.ptr(out), _C.out_dtype_code(out_dtype), gran, int(num_cu or 0), _C.ptr(ws),
         0 if ws is None else ws.numel(), _C.stream(a.device),
     )
@@ -90,9 +96,30 @@ def grouped_gemm_fp8_variable_k_impl(
     a [M_total, OUT_M], b [M_total, OUT_N].  Blockwise requires 128-aligned
     segments with scales [M_total/128, OUT_*]; rowwise takes per-column scales
     [OUT_*]; tensorwise takes scalars.
+
+    MX_BLOCKWISE follows the reference's MX wgrad call
+    (ops/grouped_gemm_fp8.py:760-775): a and b are the colwise quantized
+    tensors, already transposed and padded per group, a [OUT_M, K_pad],
+    b [OUT_N, K_pad] with E8M0 scales [OUT_*, K_pad/32] and 128-aligned
+    group_offs; out[g] = a[:, seg_g] @ b[:, seg_g]^T.
     """
-    assert trans_a and not trans_b, "variable-K grouped GEMM expects trans_a=True, trans_b=False"
     gran = _gran_code(granularity)
+    if gran == ScalingGranularity.MX_BLOCKWISE.value:
+        a = a.contiguous()
+        b = b.contiguous()
+        OUT_M, K_pad = a.shape
+        OUT_N = b.shape[0]
+        assert b.shape[1] == K_pad, "padded K mismatch"
+        G = group_lens.shape[0]
+        out = torch.empty((G, OUT_N, OUT_M) if trans_c else (G, OUT_M, OUT_N), dtype=out_dtype, device=a.device)
+        offs = group_offs.to(torch.int64).contiguous()
+        _C.call(
+            "pta_grouped_gemm_fp8_variable_k_nt", _C.ptr(a), _C.fp8_code(a.dtype), _C.ptr(_scale(a_scales, gran)),
+            _C.ptr(b), _C.fp8_code(b.dtype), _C.ptr(_scale(b_scales, gran)), _C.ptr(offs), G, K_pad, OUT_M, OUT_N,
+            _C.ptr(out), _C.out_dtype_code(out_dtype), int(trans_c), gran, _C.stream(a.device),
+        )
+        return out
+    assert trans_a and not trans_b, "variable-K grouped GEMM expects trans_a=True, trans_b=False"
     a = a.contiguous()
     b = b.contiguous()
     M_total, OUT_M = a.shape

@@ -318,6 +318,70 @@ def quantize_mxfp8_impl(
     return tuple(outs)
 
 
+def grouped_quantize_mxfp8_impl(
+    x: torch.Tensor,
+    out_dtype: torch.dtype,
+    axis: Optional[int],
+    block_size: int,
+    group_lens: torch.Tensor,
+    group_offs: torch.Tensor,
+    with_trans: bool = False,
+    scaling_recipe: Optional[ScalingRecipe] = None,
+    scaling_recipe_for_trans: Optional[ScalingRecipe] = None,
+):
+    """MXFP8 quantization of grouped rows with per-group M padding (32 rowwise,
+    128 colwise), padded layouts computed on the device
+    (reference: quantization_impl.py:546-612, quantization.cpp:969-1195).
+
+    with_trans: (q_row [M_pad_row, N_pad], s_row, q_col [N, M_pad_col], s_col,
+    group_lens_padded_rowwise, group_offs_padded_rowwise,
+    group_lens_padded_colwise, group_offs_padded_colwise).
+    axis 1 (rowwise) / 0 (colwise): (q, s, group_lens_padded, group_offs_padded).
+    """
+    _check_hp(x)
+    assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
+    assert x.dtype in (torch.bfloat16, torch.float16), "Input must be BFloat16 or Half"
+    assert x.dim() == 2 and x.is_contiguous(), "Input must be a contiguous 2D tensor"
+    rr = _check_recipe(scaling_recipe)
+    rc = _check_recipe(scaling_recipe_for_trans) if with_trans else rr
+    if rr.use_2d_block or rc.use_2d_block:
+        raise NotImplementedError("2-D exponent blocks are not implemented for grouped MXFP8 quantization")
+    M, N = x.shape
+    assert N % MXFP8_BLOCK_SIZE == 0, f"N must be divisible by {MXFP8_BLOCK_SIZE}"
+    G = group_lens.numel()
+    dev = x.device
+    if with_trans:
+        row, col = True, True
+    else:
+        assert axis in (0, 1), "The axis must be 0 or 1 when with_trans is False."
+        row, col = axis == 1, axis == 0
+    Mr = ceil_div(M + G * 32, 32) * 32
+    Mc = ceil_div(M + G * 128, 128) * 128
+    Np = ceil_div(N, 128) * 128
+    lens = group_lens.to(torch.int64).contiguous()
+    offs = group_offs.to(torch.int64).contiguous()
+    lr, orw = torch.empty_like(lens), torch.empty(G + 1, dtype=torch.int64, device=dev)
+    lc, oc = torch.empty_like(lens), torch.empty(G + 1, dtype=torch.int64, device=dev)
+    q_row = e_row = q_col = e_col = None
+    if row:
+        q_row = torch.empty((Mr, Np), dtype=out_dtype, device=dev)
+        e_row = torch.empty((Mr, Np // 32), dtype=torch.uint8, device=dev)
+    if col:
+        q_col = torch.empty((N, Mc), dtype=out_dtype, device=dev)
+        e_col = torch.empty((N, Mc // 32), dtype=torch.uint8, device=dev)
+    _C.call(
+        "pta_grouped_quantize_mxfp8", _C.ptr(x), _C.in_dtype_code(x.dtype), M, N, G, _C.ptr(lens), _C.ptr(offs),
+        _C.ptr(q_row), _C.ptr(e_row), 0, _C.ptr(lr), _C.ptr(orw), _C.ptr(q_col), _C.ptr(e_col), 0, _C.ptr(lc),
+        _C.ptr(oc), _C.fp8_code(out_dtype), _C.stream(dev),
+    )
+    e8 = torch.float8_e8m0fnu
+    if with_trans:
+        return q_row, e_row.view(e8), q_col, e_col.view(e8), lr, orw, lc, oc
+    if row:
+        return q_row, e_row.view(e8), lr, orw
+    return q_col, e_col.view(e8), lc, oc
+
+
 def dequantize_mxfp8_impl(
     x: torch.Tensor, out_dtype: torch.dtype, axis: int, block_size: int, scale_inv: torch.Tensor
 ) -> torch.Tensor:

@@ -14,6 +14,7 @@ from primus_turbo.pytorch.core.low_precision import (
     Float8QuantConfig,
     Format,
     ScalingGranularity,
+    ScalingRecipe,
     float8_e4m3,
     float8_e5m2,
 )
@@ -28,8 +29,10 @@ from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_fp8_impl import (
 )
 from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
 from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+    grouped_quantize_mxfp8_impl,
     quant_fp8_blockwise_for_weight_impl,
     quant_fp8_blockwise_segment_m_row_col_impl,
+    quantize_mxfp8_impl,
     transpose_fp8,
 )
 
@@ -188,6 +191,50 @@ class FP8GroupedGemmTensorFunc(torch.autograd.Function):
         return grad_a, grad_b, None, None, None, None, None, None, None, None
 
 
+class FP8GroupedGemmMXFunc(torch.autograd.Function):
+    """MX_BLOCKWISE (grouped_gemm_fp8.py:593-795), NT only: activations in the
+    32-row-padded grouped layout (1 x 32 exponents), weights with 32 x 32
+    exponents; the forward and dgrad read padded rows and write the packed rows
+    given by group_offs; wgrad is variable-K over the 128-padded colwise copies."""
+
+    @staticmethod
+    def forward(ctx, a, b, group_lens, group_offs, trans_b, out_dtype, config, num_cu):
+        assert config.granularity == ScalingGranularity.MX_BLOCKWISE
+        assert a.ndim == 2 and b.ndim == 3
+        assert trans_b, "MXFP8 grouped GEMM only supports trans_b=True (NT layout)."
+        if isinstance(a, QuantizedTensor):
+            a = a.dequantize()
+        if isinstance(b, QuantizedTensor):
+            b = b.dequantize()
+        a_dtype = _get_fp8_dtype(config.format, True)
+        bs = config.block_size
+        a_row, a_srow, a_col, a_scol, _, offs_pad_row, _, _ = grouped_quantize_mxfp8_impl(
+            a.contiguous(), a_dtype, None, bs, group_lens, group_offs, True)
+        b_row, b_srow, b_col, b_scol = quantize_mxfp8_impl(
+            b.contiguous(), a_dtype, None, bs, with_trans=True, scaling_recipe=ScalingRecipe(use_2d_block=True),
+            scaling_recipe_for_trans=ScalingRecipe(use_2d_block=True))
+        total_m = a.size(0)
+        out = grouped_gemm_fp8_impl(a_row, b_row, a_srow, b_srow, group_lens, offs_pad_row, False, True, out_dtype,
+                                    ScalingGranularity.MX_BLOCKWISE.value, num_cu, group_offs_out=group_offs)
+        out = out[:total_m]
+        ctx.save_for_backward(a_col, a_scol, b_col, b_scol, group_lens, group_offs)
+        ctx.config, ctx.out_dtype, ctx.num_cu, ctx.total_m = config, out_dtype, num_cu, total_m
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        a_col, a_scol, b_col, b_scol, group_lens, group_offs = ctx.saved_tensors
+        g_dtype = _get_fp8_dtype(ctx.config.format, False)
+        mx = ScalingGranularity.MX_BLOCKWISE.value
+        g_row, g_srow, g_col, g_scol, _, offs_pad_row, lens_pad_col, offs_pad_col = grouped_quantize_mxfp8_impl(
+            grad_out.contiguous(), g_dtype, None, ctx.config.block_size, group_lens, group_offs, True)
+        grad_a = grouped_gemm_fp8_impl(g_row, b_col, g_srow, b_scol, group_lens, offs_pad_row, False, True,
+                                       ctx.out_dtype, mx, ctx.num_cu, group_offs_out=group_offs)[: ctx.total_m]
+        grad_b = grouped_gemm_fp8_variable_k_impl(g_col, a_col, g_scol, a_scol, lens_pad_col, offs_pad_col, False,
+                                                  False, False, ctx.out_dtype, mx, ctx.num_cu)
+        return grad_a, grad_b, None, None, None, None, None, None
+
+
 @torch._dynamo.disable(recursive=True)
 def grouped_gemm_fp8(
     a: Union[torch.Tensor, QuantizedTensor, QuantizedTensorPair],
@@ -221,5 +268,5 @@ def grouped_gemm_fp8(
     elif config.granularity == ScalingGranularity.BLOCKWISE:
         return FP8GroupedGemmBlockFunc.apply(a, b, group_lens, group_offs, trans_b, out_dtype, config, num_cu)
     elif config.granularity == ScalingGranularity.MX_BLOCKWISE:
-        raise NotImplementedError("grouped MX_BLOCKWISE GEMM is not implemented in this build")
+        return FP8GroupedGemmMXFunc.apply(a_data, b_data, group_lens, group_offs, trans_b, out_dtype, config, num_cu)
     raise ValueError(f"Unsupported FP8 ScalingGranularity: {config.granularity}")

@@ -18,6 +18,7 @@ from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
     dequantize_fp8_rowwise_impl,
     dequantize_fp8_tensorwise_impl,
     dequantize_mxfp8_impl,
+    grouped_quantize_mxfp8_impl,
     quant_fp8_blockwise_dual_impl,
     quant_fp8_blockwise_for_weight_impl,
     quant_fp8_blockwise_impl,
@@ -99,7 +100,13 @@ def grouped_quantize_fp8(
     axis: Optional[int] = None,
     scaling_recipe: Optional[ScalingRecipe] = None,
 ):
-    raise NotImplementedError("grouped MXFP8 quantization is not implemented in this build")
+    """Grouped MXFP8 quantization along one axis (ops/quantization.py:144-180):
+    returns (q, scale, group_lens_padded, group_offs_padded)."""
+    if granularity == ScalingGranularity.MX_BLOCKWISE:
+        assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
+        return grouped_quantize_mxfp8_impl(x, out_dtype, axis, block_size, group_lens, group_offs, False,
+                                           scaling_recipe)
+    raise NotImplementedError(f"Unknown granularity {granularity}")
 
 
 def grouped_quantize_fp8_with_trans(
@@ -113,7 +120,14 @@ def grouped_quantize_fp8_with_trans(
     scaling_recipe: Optional[ScalingRecipe] = None,
     scaling_recipe_for_trans: Optional[ScalingRecipe] = None,
 ):
-    raise NotImplementedError("grouped MXFP8 quantization is not implemented in this build")
+    """Grouped MXFP8 rowwise + colwise quantization (ops/quantization.py:183-222):
+    returns (q_row, s_row, q_col, s_col, group_lens_padded_rowwise,
+    group_offs_padded_rowwise, group_lens_padded_colwise, group_offs_padded_colwise)."""
+    if granularity == ScalingGranularity.MX_BLOCKWISE:
+        assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
+        return grouped_quantize_mxfp8_impl(x, out_dtype, None, block_size, group_lens, group_offs, True,
+                                           scaling_recipe, scaling_recipe_for_trans)
+    raise NotImplementedError(f"Unknown granularity {granularity}")
 
 
 def dequantize_fp8(

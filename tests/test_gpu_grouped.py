@@ -117,13 +117,18 @@ def test_grouped_variable_k_blockwise_vs_oracle(lens, trans_c):
 
 
 @pytest.mark.parametrize("lens", [[300, 0, 513, 128, 59], [64, 64, 64, 64]])
-@pytest.mark.parametrize("gran", ["BLOCKWISE", "TENSORWISE", "ROWWISE"])
+@pytest.mark.parametrize("gran", ["BLOCKWISE", "TENSORWISE", "ROWWISE", "MX_BLOCKWISE"])
 def test_grouped_gemm_fp8_autograd(lens, gran):
     """The reference's grouped criterion: SNR vs a per-group fp32 matmul
     (tests/pytorch/ops/test_grouped_gemm_fp8.py:163-175)."""
     (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
     g = getattr(SG, gran)
-    cfg = Cfg(granularity=g, format=Format.E4M3, block_size=128 if gran == "BLOCKWISE" else None)
+    if gran == "MX_BLOCKWISE":
+        from primus_turbo.pytorch.core.low_precision import ScaleDtype
+
+        cfg = Cfg(granularity=g, format=Format.E4M3, block_size=32, scale_dtype=ScaleDtype.E8M0)
+    else:
+        cfg = Cfg(granularity=g, format=Format.E4M3, block_size=128 if gran == "BLOCKWISE" else None)
     G, K, N = len(lens), 512, 256
     M = sum(lens)
     gen = torch.Generator().manual_seed(0)
@@ -144,3 +149,85 @@ def test_grouped_gemm_fp8_autograd(lens, gran):
     for name, x, r in (("out", out, ref), ("dA", a.grad, a_ref.grad), ("dW", w.grad, w_ref.grad)):
         s = O.snr_db(f32(r), f32(x))
         assert s > 25, f"{name} SNR {s:.1f} dB"
+
+
+MX_LENS = [[300, 0, 513, 128, 59], [0, 0, 256], [33], [64, 64, 64, 64]]
+
+
+@pytest.mark.parametrize("lens", MX_LENS)
+@pytest.mark.parametrize("dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_grouped_mx_quant_vs_oracle(lens, dtype):
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import grouped_quantize_mxfp8_impl
+
+    M, N = sum(lens), 160
+    gen = torch.Generator().manual_seed(9)
+    x = (torch.exp(torch.randn((max(M, 1), N), generator=gen) * 1.5) * torch.sign(torch.randn((max(M, 1), N), generator=gen)))
+    x = x[:M].bfloat16().contiguous()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = group_offs_from_lens(gl)
+    q_row, e_row, q_col, e_col, lr, orw, lc, oc = grouped_quantize_mxfp8_impl(x.cuda(), dtype, None, 32, gl, go, True)
+    f = 0 if dtype == torch.float8_e4m3fn else 1
+    rq, re, rorw, cq, ce, roc = O.quant_mx_grouped(x, f, lens)
+    assert np.array_equal(orw.cpu().numpy(), rorw) and np.array_equal(oc.cpu().numpy(), roc)
+    assert np.array_equal(lr.cpu().numpy(), np.diff(rorw)) and np.array_equal(lc.cpu().numpy(), np.diff(roc))
+    R, C = int(rorw[-1]), int(roc[-1])
+    assert np.array_equal(u8(q_row)[:R], rq[:R]) and np.array_equal(u8(e_row)[:R], re[:R])
+    assert np.array_equal(u8(q_col)[:, :C], cq[:, :C]) and np.array_equal(u8(e_col)[:, : C // 32], ce[:, : C // 32])
+
+
+@pytest.mark.parametrize("lens", MX_LENS)
+def test_grouped_mx_gemm_fwd_and_wgrad_vs_oracle(lens):
+    """Forward reads the 32-padded rows and writes packed rows (group_offs_out);
+    the variable-K wgrad runs on the 128-padded colwise copies."""
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity as SG
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_fp8_impl import (
+        grouped_gemm_fp8_impl,
+        grouped_gemm_fp8_variable_k_impl,
+    )
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        grouped_quantize_mxfp8_impl,
+        quantize_mxfp8_impl,
+    )
+    from primus_turbo.pytorch.core.low_precision import ScalingRecipe
+
+    G, K, N = len(lens), 256, 192
+    M = sum(lens)
+    a = randn((max(M, 1), K), seed=31)[:M].contiguous()
+    w = randn((G, N, K), seed=32, scale=0.05)
+    dy = randn((max(M, 1), N), seed=33)[:M].contiguous()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = group_offs_from_lens(gl)
+    e4 = torch.float8_e4m3fn
+    mx = SG.MX_BLOCKWISE.value
+    a_row, a_srow, a_col, a_scol, _, orw, _, _ = grouped_quantize_mxfp8_impl(a.cuda(), e4, None, 32, gl, go, True)
+    w_row, w_srow = quantize_mxfp8_impl(w.cuda(), e4, 2, 32, scaling_recipe=ScalingRecipe(use_2d_block=True))
+    out = grouped_gemm_fp8_impl(a_row, w_row, a_srow, w_srow, gl, orw, False, True, torch.bfloat16, mx,
+                                group_offs_out=go)
+    assert out.shape[0] >= M
+    da = O.dequant_mx(u8(a_row), 0, u8(a_srow))
+    dw = O.dequant_mx(u8(w_row).reshape(G * N, -1), 0, u8(w_srow).reshape(G * N, -1)).reshape(G, N, -1)
+    o = f32(out)
+    orw_h = orw.cpu().numpy()
+    s = 0
+    for g, L in enumerate(lens):
+        if L:
+            ref = O.gemm_ref(da[orw_h[g]:orw_h[g] + L], dw[g], False, True)
+            _check(o[s:s + L], ref, f"fwd group {g}")
+        s += L
+    # wgrad: dW[g] = dy_g^T a_g over the 128-padded colwise copies
+    g_row, g_srow, g_col, g_scol, _, _, lc, oc = grouped_quantize_mxfp8_impl(dy.cuda(), e4, None, 32, gl, go, True)
+    dW = grouped_gemm_fp8_variable_k_impl(g_col, a_col, g_scol, a_scol, lc, oc, False, False, False,
+                                          torch.bfloat16, mx)
+    assert tuple(dW.shape) == (G, N, K)
+    dgc = O.dequant_mx(u8(g_col), 0, u8(g_scol))
+    dac = O.dequant_mx(u8(a_col), 0, u8(a_scol))
+    oc_h = oc.cpu().numpy()
+    w_out = f32(dW)
+    for g in range(G):
+        c0, c1 = oc_h[g], oc_h[g + 1]
+        if c1 == c0:
+            assert not w_out[g].any()
+            continue
+        _check(w_out[g], O.gemm_ref(dgc[:, c0:c1], dac[:, c0:c1], False, True), f"wgrad group {g}")

@@ -241,3 +241,33 @@ def test_reference_roundtrip_tolerance():
     for axis in (0, 1):
         q, s = O.quant_block1d(x, 0, axis)
         np.testing.assert_allclose(O.dequant_block1d(q, 0, s, axis), xf, rtol=0.1, atol=0.1)
+
+
+def test_grouped_mx_layout_and_locality():
+    """Grouped MXFP8 layout (reference quantization.cpp:969-1195): per-group
+    rows padded to 32 (rowwise) / 128 (colwise) with exclusive-prefix offsets;
+    rowwise bytes of a group equal the ungrouped rowwise quantization of its
+    rows; padding is zero; a colwise block never sees another group's rows."""
+    import torch
+
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(330, 96, generator=g) * 4).bfloat16()
+    lens = [100, 0, 37, 193]
+    qr, er, orw, qc, ec, oc = O.quant_mx_grouped(x, 0, lens)
+    assert list(orw) == [0, 128, 128, 192, 416]
+    assert list(oc) == [0, 128, 128, 256, 512]
+    assert qr.shape == ((330 + 4 * 32 + 31) // 32 * 32, 128) and qc.shape == (96, (330 + 4 * 128 + 127) // 128 * 128)
+    s = 0
+    for gi, L in enumerate(lens):
+        if L:
+            q0, e0 = O.quant_mx(x[s:s + L], 0, 1)
+            assert np.array_equal(qr[orw[gi]:orw[gi] + L], q0) and np.array_equal(er[orw[gi]:orw[gi] + L], e0)
+            assert not qr[orw[gi] + L:orw[gi + 1]].any() and not er[orw[gi] + L:orw[gi + 1]].any()
+            assert not qc[:, oc[gi] + L:oc[gi + 1]].any()
+        s += L
+    # locality: scaling group 3 by 2^10 leaves every colwise byte / exponent of groups 0-2 unchanged
+    y = x.clone()
+    y[137:] = (y[137:].float() * 1024).bfloat16()
+    _, _, _, qc2, ec2, _ = O.quant_mx_grouped(y, 0, lens)
+    assert np.array_equal(qc2[:, :256], qc[:, :256]) and np.array_equal(ec2[:, :8], ec[:, :8])
+    assert not np.array_equal(ec2[:, 8:16], ec[:, 8:16])
