@@ -240,3 +240,33 @@ def test_gemm_multi_round_wgrad_1d_scales():
     db = O.dequant_block1d(u8(qb), 0, f32(sb), 0)
     out = gemm_fp8_impl(qa, sa, True, qb, sb, False, torch.bfloat16, False, g.value)
     _check(out, O.gemm_ref(da, db, True, False), "TN multi-round")
+
+
+@pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
+def test_float8_linear_fwd_bwd(gran):
+    """Float8Linear on a [2, 96, 512] input against an fp32 Linear (reference's
+    SNR criterion, > 25 dB for e4m3), bias and leading dims included."""
+    turbo, Cfg, Format, ScaleDtype, SG, _, _ = _mods()
+    g = getattr(SG, gran)
+    kw = {}
+    if g == SG.BLOCKWISE:
+        kw = dict(block_size=128)
+    elif g == SG.MX_BLOCKWISE:
+        kw = dict(block_size=32, scale_dtype=ScaleDtype.E8M0)
+    cfg = Cfg(granularity=g, format=Format.E4M3, **kw)
+    torch.manual_seed(3)
+    ref = torch.nn.Linear(512, 256, bias=True).cuda()
+    lin = turbo.modules.Float8Linear.from_float(ref, cfg, inplace=False).to(torch.bfloat16)
+    x = torch.randn(2, 96, 512, device="cuda")
+    xb = x.bfloat16().requires_grad_()
+    y = lin(xb)
+    assert y.shape == (2, 96, 256) and y.dtype == torch.bfloat16
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    xr = xb.detach().float().requires_grad_()
+    yr = torch.nn.functional.linear(xr, lin.weight.detach().float(), lin.bias.detach().float())
+    yr.backward(dy.float())
+    for name, a, r in (("y", y, yr), ("dx", xb.grad, xr.grad)):
+        s = O.snr_db(f32(r), f32(a))
+        assert s > 25, f"{name} SNR {s:.1f} dB"
+    assert lin.weight.grad is not None and lin.weight.grad.shape == lin.weight.shape

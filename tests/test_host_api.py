@@ -67,3 +67,23 @@ def test_gemm_fp8_shape_asserts():
 
     with pytest.raises(AssertionError, match="2D"):
         turbo.ops.gemm_fp8(torch.zeros(2, 2, 2), torch.zeros(2, 2))
+
+
+def test_float8_linear_conversion():
+    """Float8Linear.from_float keeps the parameters (in place) or copies them."""
+    import torch
+
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import Float8QuantConfig, ScalingGranularity
+
+    lin = torch.nn.Linear(64, 32, bias=True)
+    w = lin.weight.detach().clone()
+    cfg = Float8QuantConfig(granularity=ScalingGranularity.BLOCKWISE, block_size=128)
+    new = turbo.modules.Float8Linear.from_float(lin, cfg, inplace=False)
+    assert isinstance(new, turbo.modules.Float8Linear) and new.config is cfg
+    assert torch.equal(new.weight, w) and torch.equal(new.bias, lin.bias)
+    assert type(lin) is torch.nn.Linear
+    same = turbo.modules.Float8Linear.from_float(lin)
+    assert same is lin and isinstance(lin, turbo.modules.Float8Linear)
+    assert lin.config.granularity == ScalingGranularity.TENSORWISE
+    assert "config=" in repr(lin)
