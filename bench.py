@@ -151,13 +151,14 @@ def main():
     SG = ScalingGranularity
 
     # ---- quantized operands (resident in HBM) ------------------------------
-    a_row, a_s, _, _ = quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True)
+    # the activation layout gemm_fp8's forward produces (row scales K-block major)
+    a_row, a_s, _, _ = quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True, row_scale_kmajor=True)
     w_q, w_s = quant_fp8_blockwise_for_weight_impl(w, fdt, 128)
     nbk = K // 128
     out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
     def gemm():
-        gemm_fp8_nt(a_row, w_q, torch.bfloat16, SG.BLOCKWISE, a_s, (nbk, 1), False, w_s, (nbk, 1), True, out=out)
+        gemm_fp8_nt(a_row, w_q, torch.bfloat16, SG.BLOCKWISE, a_s, a_s.stride(), False, w_s, (nbk, 1), True, out=out)
 
     ms = _time_cuda(gemm, args.steps, args.warmup)
     flops = 2.0 * M * N * K
@@ -294,11 +295,11 @@ def _other_configs(args):
     # config 3, shape 2: blockwise 4096 x 2048 @ [7168 x 2048]^T
     a3 = torch.randn((4096, 2048), generator=g).bfloat16().to(dev)
     w3 = torch.randn((7168, 2048), generator=g).bfloat16().to(dev)
-    ar3, as3, _, _ = quant_fp8_blockwise_dual_impl(a3, e4, 128, col_transposed=True)
+    ar3, as3, _, _ = quant_fp8_blockwise_dual_impl(a3, e4, 128, col_transposed=True, row_scale_kmajor=True)
     wq3, ws3 = quant_fp8_blockwise_for_weight_impl(w3, e4, 128)
     o3 = torch.empty((4096, 7168), dtype=torch.bfloat16, device=dev)
     res["cfg3_blockwise_4096x7168x2048_NT"] = {
-        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_nt(ar3, wq3, torch.bfloat16, SG.BLOCKWISE, as3, (16, 1), False,
+        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_nt(ar3, wq3, torch.bfloat16, SG.BLOCKWISE, as3, as3.stride(), False,
                                                          ws3, (16, 1), True, out=o3), it, 3), 2.0 * 4096 * 7168 * 2048),
     }
     del a3, w3, ar3, wq3, o3
@@ -358,8 +359,8 @@ def _extras(args, a, w, grad, M, N, K, flops):
     nbk = K // 128
 
     # ---- quantize kernels ----------------------------------------------------
-    def q_act():
-        quant_fp8_blockwise_dual_impl(a, fdt, 128)
+    def q_act():  # the layout of gemm_fp8's forward
+        quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True, row_scale_kmajor=True)
 
     def q_w():
         quant_fp8_blockwise_for_weight_impl(w, fdt, 128)
@@ -385,7 +386,8 @@ def _extras(args, a, w, grad, M, N, K, flops):
     step_ms = _time_cuda(train_step, max(3, args.steps // 5), 2)
 
     # ---- layouts of the backward GEMMs, timed alone -------------------------
-    g_row, g_s, g_colT, g_cs = quant_fp8_blockwise_dual_impl(grad, fdt, 128, col_transposed=True)
+    g_row, g_s, g_colT, g_cs = quant_fp8_blockwise_dual_impl(grad, fdt, 128, col_transposed=True,
+                                                              row_scale_kmajor=True)
     _, _, a_colT, a_cs = quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True)
     _, w_s, w_t = quant_fp8_blockwise_for_weight_impl(w, fdt, 128, with_transpose=True)
     da = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
@@ -393,7 +395,7 @@ def _extras(args, a, w, grad, M, N, K, flops):
     nbn = N // 128
 
     def dgrad():
-        gemm_fp8_nt(g_row, w_t, torch.bfloat16, SG.BLOCKWISE, g_s, (nbn, 1), False, w_s, (1, nbk), True, out=da)
+        gemm_fp8_nt(g_row, w_t, torch.bfloat16, SG.BLOCKWISE, g_s, g_s.stride(), False, w_s, (1, nbk), True, out=da)
 
     def wgrad():
         gemm_fp8_nt(g_colT, a_colT, torch.bfloat16, SG.BLOCKWISE, g_cs, (1, N), False, a_cs, (1, K), False, out=dw)

@@ -89,15 +89,22 @@ int pta_quantize_fp8_rowwise(const void *x, int in_dtype, int64_t outer, int64_t
 int pta_quantize_fp8_blockwise(const void *x, int in_dtype, int64_t M, int64_t N, int64_t block,
                                int axis, void *q, float *s, int fmt, pta_stream_t stream);
 
+/* Layout flags of pta_quantize_fp8_blockwise_dual. */
+#define PTA_DUAL_COL_TRANSPOSED 1   /* q_col written as [N, roundup(M, 128)], zero padded */
+#define PTA_DUAL_ROW_SCALE_KMAJOR 2 /* s_row written as [ceil(N/block), M] */
+
 /* Blockwise dual (one read of x): row-scaled q_row[M,N] + s_row[M, ceil(N/block)]
- * and col-scaled q_col + s_col[ceil(M/block), N].  col_transposed = 0 writes
- * q_col as [M, N] (the reference layout); 1 writes it as [N, M_pad] with
- * M_pad = roundup(M, 128) and zero padding (K-contiguous operand for the NT
- * wgrad GEMM).  Either output pair may be NULL.
+ * and col-scaled q_col + s_col[ceil(M/block), N].  Without flags q_col is
+ * [M, N] and s_row is [M, ceil(N/block)] (the reference layouts).
+ * PTA_DUAL_COL_TRANSPOSED writes q_col as [N, M_pad], M_pad = roundup(M, 128),
+ * zero padded (K-contiguous operand for the NT wgrad GEMM);
+ * PTA_DUAL_ROW_SCALE_KMAJOR stores s_row(m, kb) at s_row[kb * M + m], so a GEMM
+ * reading the scales of one K block for consecutive rows touches consecutive
+ * words.  Either output pair may be NULL.
  * Replaces quant_fp8_blockwise_dual_impl (quantization_impl.py:229-274). */
 int pta_quantize_fp8_blockwise_dual(const void *x, int in_dtype, int64_t M, int64_t N,
                                     int64_t block, void *q_row, float *s_row, void *q_col,
-                                    float *s_col, int col_transposed, int fmt, pta_stream_t stream);
+                                    float *s_col, int layout, int fmt, pta_stream_t stream);
 
 /* Blockwise 2-D weight quant: w[B, M, N] -> q[B, M, N],
  * s[B, ceil(M/block), ceil(N/block)], one scale per block x block tile.

@@ -36,7 +36,8 @@ struct QBArgs {
     int64_t     M, N;      // input rows / cols (per batch for W2D)
     int64_t     batch_stride_x;
     uint8_t    *q_row;     // ROW / W2D output
-    float      *s_row;     // ROW: [M, nb] (non-segment) or [nb, M] (segment)
+    float      *s_row;     // ROW: s_row[r * srow_m + kb * srow_k]
+    int64_t     srow_m, srow_k;
     uint8_t    *q_col;     // COL output
     float      *s_col;     // COL: [mb, N]
     uint8_t    *q_t;       // W2D_T output
@@ -162,7 +163,6 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
 
     // ---- row direction ----------------------------------------------------
     if constexpr ((MODE & QB_ROW) != 0) {
-        const int64_t nb = (N + TILE - 1) / TILE;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float a = 0.0f;
@@ -185,8 +185,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                         if (n0 + j < N) dst[j] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
                 }
                 if (cseg == 0) {
-                    if constexpr ((MODE & QB_SEGMENT) != 0) args.s_row[tn * M + r] = sinv;
-                    else args.s_row[r * nb + tn] = sinv;
+                    args.s_row[r * args.srow_m + tn * args.srow_k] = sinv;
                 }
             }
         }
@@ -459,6 +458,7 @@ extern "C" int pta_quantize_fp8_blockwise(const void *x, int in_dtype, int64_t M
     const bool v = vec_ok(x, in_dtype, N, {q});
     if (axis == 1) {
         a.q_row = static_cast<uint8_t *>(q); a.s_row = s;
+        a.srow_m = cdiv(N, TILE); a.srow_k = 1;
         return launch_tile<QB_ROW>(a, in_dtype, fmt, grid, v, as_stream(stream));
     }
     a.q_col = static_cast<uint8_t *>(q); a.s_col = s;
@@ -467,7 +467,7 @@ extern "C" int pta_quantize_fp8_blockwise(const void *x, int in_dtype, int64_t M
 
 extern "C" int pta_quantize_fp8_blockwise_dual(const void *x, int in_dtype, int64_t M, int64_t N,
                                                int64_t block, void *q_row, float *s_row,
-                                               void *q_col, float *s_col, int col_transposed,
+                                               void *q_col, float *s_col, int layout,
                                                int fmt, pta_stream_t stream) {
     clear_error();
     if (int rc = check_common(x, in_dtype, fmt, block)) return rc;
@@ -475,10 +475,14 @@ extern "C" int pta_quantize_fp8_blockwise_dual(const void *x, int in_dtype, int6
     PTA_CHECK_ARG((q_row == nullptr) == (s_row == nullptr), "q_row/s_row must both be set or NULL");
     PTA_CHECK_ARG((q_col == nullptr) == (s_col == nullptr), "q_col/s_col must both be set or NULL");
     PTA_CHECK_ARG(q_row || q_col, "no output requested");
+    PTA_CHECK_ARG((layout & ~(PTA_DUAL_COL_TRANSPOSED | PTA_DUAL_ROW_SCALE_KMAJOR)) == 0, "unknown layout flags");
     if (M == 0 || N == 0) return PTA_OK;
-    QBArgs a{};
+    const bool col_transposed = (layout & PTA_DUAL_COL_TRANSPOSED) != 0;
+    QBArgs     a{};
     a.x = x; a.M = M; a.N = N;
     a.q_row = static_cast<uint8_t *>(q_row); a.s_row = s_row;
+    if (layout & PTA_DUAL_ROW_SCALE_KMAJOR) { a.srow_m = 1; a.srow_k = M; }
+    else { a.srow_m = cdiv(N, TILE); a.srow_k = 1; }
     a.q_col = static_cast<uint8_t *>(q_col); a.s_col = s_col;
     dim3       grid(static_cast<uint32_t>(cdiv(M, TILE)), static_cast<uint32_t>(cdiv(N, TILE)), 1);
     PTA_CHECK_ARG(!col_transposed || aligned16(q_col), "transposed q_col must be 16-byte aligned");
@@ -532,6 +536,7 @@ extern "C" int pta_quantize_fp8_blockwise_segment_m_row_col(
     QBArgs        a{};
     a.x = x; a.M = M; a.N = N;
     a.q_row = static_cast<uint8_t *>(q_row); a.s_row = s_row_t;
+    a.srow_m = 1; a.srow_k = M;
     a.q_col = static_cast<uint8_t *>(q_col_pad); a.s_col = s_col_pad;
     a.group_offs = group_offs; a.padded_offs = vk_offs; a.G = G;
     dim3 grid(static_cast<uint32_t>(cdiv(M_pad_max, TILE)), static_cast<uint32_t>(cdiv(N, TILE)), 1);

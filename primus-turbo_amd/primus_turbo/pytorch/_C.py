@@ -17,6 +17,8 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file_
 PTA_F32, PTA_F16, PTA_BF16 = 0, 1, 2
 PTA_E4M3, PTA_E5M2 = 0, 1
 PTA_TENSORWISE, PTA_ROWWISE, PTA_BLOCKWISE, PTA_MX_BLOCKWISE = 1, 2, 3, 4
+# layout flags of pta_quantize_fp8_blockwise_dual
+DUAL_COL_TRANSPOSED, DUAL_ROW_SCALE_KMAJOR = 1, 2
 
 _vp, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
 

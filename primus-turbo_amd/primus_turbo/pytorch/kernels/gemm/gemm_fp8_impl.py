@@ -38,6 +38,20 @@ def _scale_arg(s: torch.Tensor, gran: int) -> torch.Tensor:
     return s.contiguous().to(torch.float32)
 
 
+def _strided_scale_arg(s: torch.Tensor, gran: int) -> Tuple[torch.Tensor, int]:
+    """Scale storage for explicitly strided addressing (layout kept) and the
+    byte extent the kernel may read."""
+    if gran == ScalingGranularity.MX_BLOCKWISE.value:
+        s = s.contiguous().view(torch.uint8)
+        return s, s.numel()
+    if s.dtype != torch.float32:
+        s = s.to(torch.float32)
+    if s.numel() == 0:
+        return s, 0
+    last = sum((d - 1) * st for d, st in zip(s.shape, s.stride()))
+    return s, (last + 1) * 4
+
+
 def gemm_fp8_impl(
     a: torch.Tensor,
     a_scale_inv: torch.Tensor,
@@ -102,14 +116,15 @@ def gemm_fp8_nt(
         K = a.shape[1]
     assert a.shape[1] >= K and b.shape[1] >= K, "operands shorter than K"
     # columns past K (if any) are never read
-    sa = _scale_arg(a_scale, gran)
-    sb = _scale_arg(b_scale, gran)
+    # the strides address the scale storage as it is laid out (no reordering copy)
+    sa, sa_bytes = _strided_scale_arg(a_scale, gran)
+    sb, sb_bytes = _strided_scale_arg(b_scale, gran)
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=a.device)
     _C.call(
         "pta_gemm_fp8_nt_strided", _C.ptr(a), _C.fp8_code(a.dtype), a.stride(0), _C.ptr(b), _C.fp8_code(b.dtype),
         b.stride(0), _C.ptr(out), _C.out_dtype_code(out.dtype), out.stride(0), M, N, K, gran, _C.ptr(sa),
-        sa_strides[0], sa_strides[1], int(a_scale_2d), sa.numel() * sa.element_size(), _C.ptr(sb), sb_strides[0],
-        sb_strides[1], int(b_scale_2d), sb.numel() * sb.element_size(), _C.stream(a.device),
+        sa_strides[0], sa_strides[1], int(a_scale_2d), sa_bytes, _C.ptr(sb), sb_strides[0],
+        sb_strides[1], int(b_scale_2d), sb_bytes, _C.stream(a.device),
     )
     return out

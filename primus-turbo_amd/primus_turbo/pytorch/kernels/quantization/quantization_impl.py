@@ -139,24 +139,38 @@ def quant_fp8_blockwise_impl(
 
 
 def quant_fp8_blockwise_dual_impl(
-    x: torch.Tensor, dtype: torch.dtype, block_size: int = 128, col_transposed: bool = False
+    x: torch.Tensor,
+    dtype: torch.dtype,
+    block_size: int = 128,
+    col_transposed: bool = False,
+    row_scale_kmajor: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Row (1 x bs) and column (bs x 1) quantization in one read of ``x``.
 
-    ``col_transposed=True`` (an extension used by the autograd functions) writes
-    the column-quantized bytes as ``[N, roundup(M, 128)]`` (zero padded) so the
-    wgrad GEMM reads them K-contiguously; the default is the reference's ``[M, N]``.
+    Two extensions used by the autograd functions (the defaults give the
+    reference's layouts):
+    - ``col_transposed=True`` writes the column-quantized bytes as
+      ``[N, roundup(M, 128)]`` (zero padded) so the wgrad GEMM reads them
+      K-contiguously (the reference's is ``[M, N]``);
+    - ``row_scale_kmajor=True`` returns the row scales as a ``[M, N/bs]`` view
+      of ``[N/bs, M]`` storage (strides ``(1, M)``): the GEMM then reads the
+      scales of one K block for 16 consecutive rows from one cache line.
     """
     _check_hp(x)
     assert x.is_contiguous() and x.dim() == 2, "Input must be 2D and contiguous"
     M, N = x.shape
+    nb = ceil_div(N, block_size)
     q_row = torch.empty((M, N), dtype=dtype, device=x.device)
-    s_row = torch.empty((M, ceil_div(N, block_size)), dtype=torch.float32, device=x.device)
+    if row_scale_kmajor:
+        s_row = torch.empty((nb, M), dtype=torch.float32, device=x.device).t()
+    else:
+        s_row = torch.empty((M, nb), dtype=torch.float32, device=x.device)
     q_col = torch.empty((N, ceil_div(M, 128) * 128) if col_transposed else (M, N), dtype=dtype, device=x.device)
     s_col = torch.empty((ceil_div(M, block_size), N), dtype=torch.float32, device=x.device)
+    layout = (_C.DUAL_COL_TRANSPOSED if col_transposed else 0) | (_C.DUAL_ROW_SCALE_KMAJOR if row_scale_kmajor else 0)
     _C.call(
         "pta_quantize_fp8_blockwise_dual", _C.ptr(x), _C.in_dtype_code(x.dtype), M, N, block_size, _C.ptr(q_row),
-        _C.ptr(s_row), _C.ptr(q_col), _C.ptr(s_col), int(col_transposed), _C.fp8_code(dtype), _C.stream(x.device),
+        _C.ptr(s_row), _C.ptr(q_col), _C.ptr(s_col), layout, _C.fp8_code(dtype), _C.stream(x.device),
     )
     return q_row, s_row, q_col, s_col
 

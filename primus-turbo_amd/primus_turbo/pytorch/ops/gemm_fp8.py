@@ -209,7 +209,8 @@ class FP8GemmBlockFunction(torch.autograd.Function):
             a_col_s = a_t.scale_inv
         else:
             a_row, a_row_s, a_colT, a_col_s = quant_fp8_blockwise_dual_impl(
-                a.detach().contiguous(), fdt, block_size=config.block_size, col_transposed=True
+                a.detach().contiguous(), fdt, block_size=config.block_size, col_transposed=True,
+                row_scale_kmajor=True,
             )
         # --- B: 128 x 128 blocks, reused by fwd and dgrad
         recipe = ScalingRecipe(use_2d_block=True)
@@ -230,7 +231,7 @@ class FP8GemmBlockFunction(torch.autograd.Function):
         nbn = _ceil(N, _BLOCK)
         w_str_nk = (nbk, 1) if trans_b else (1, nbn)  # rows n, blocks k
         w_str_kn = (1, nbk) if trans_b else (nbn, 1)  # rows k, blocks n
-        out = gemm_fp8_nt(a_row, w_nk, out_dtype, gran, a_row_s, (nbk, 1), False, w_s, w_str_nk, True)
+        out = gemm_fp8_nt(a_row, w_nk, out_dtype, gran, a_row_s, a_row_s.stride(), False, w_s, w_str_nk, True)
         ctx.save_for_backward(a_colT, a_col_s, _pad_cols(w_kn, _BLOCK), w_s)
         ctx.w_str_kn = w_str_kn
         ctx.trans_b, ctx.out_dtype, ctx.config = trans_b, out_dtype, config
@@ -244,11 +245,11 @@ class FP8GemmBlockFunction(torch.autograd.Function):
         M, N, K = ctx.M, ctx.N, ctx.K
         gdt = _get_fp8_dtype(ctx.config.format, False)
         g_row, g_row_s, g_colT, g_col_s = quant_fp8_blockwise_dual_impl(
-            grad_out.contiguous(), gdt, block_size=ctx.config.block_size, col_transposed=True
+            grad_out.contiguous(), gdt, block_size=ctx.config.block_size, col_transposed=True,
+            row_scale_kmajor=True,
         )
-        nbn = _ceil(N, _BLOCK)
         # dgrad: dA[M, K] = g_row[M, N] . w_kn[K, N]^T
-        grad_a = gemm_fp8_nt(_pad_cols16(g_row), w_kn, ctx.out_dtype, gran, g_row_s, (nbn, 1), False,
+        grad_a = gemm_fp8_nt(_pad_cols16(g_row), w_kn, ctx.out_dtype, gran, g_row_s, g_row_s.stride(), False,
                              w_s, ctx.w_str_kn, True)
         # wgrad over M (column-direction copies, transposed, M padded to 128)
         if ctx.trans_b:  # dW[N, K] = g_colT[N, M] . a_colT[K, M]^T

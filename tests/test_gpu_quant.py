@@ -176,6 +176,12 @@ def test_blockwise_dual_vs_oracle(shape, qdt):
     assert_bytes_equal(qct[:, :M], o[2].T, "transposed col bytes")
     assert not qct[:, M:].any(), "padding must be zero"
     assert_f32_bitexact(f32(sct), o[3], "col scales (transposed path)")
+    # K-block-major row scales: same values, storage [N/128, M]
+    qrk, srk, _, _ = quant_fp8_blockwise_dual_impl(x.cuda(), qdt, 128, col_transposed=True, row_scale_kmajor=True)
+    assert srk.shape == (M, -(-N // 128)) and srk.stride() == (1, M)
+    assert_bytes_equal(u8(qrk), o[0], "row bytes (k-major scales)")
+    assert_f32_bitexact(f32(srk), o[1], "row scales (k-major storage)")
+    assert_f32_bitexact(f32(srk.t().contiguous()).T, o[1], "k-major storage order")
 
 
 @pytest.mark.parametrize("shape", [(512, 384), (300, 260), (2, 300, 260), (4, 256, 640)])
