@@ -182,6 +182,18 @@ int pta_dequantize_fp8_blockwise(const void *q, int fmt, int64_t B, int64_t M, i
 int pta_dequantize_mxfp8(const void *q, int fmt, int64_t R, int64_t C, const uint8_t *e8m0,
                          int transpose_out, void *y, int out_dtype, pta_stream_t stream);
 
+/* Grouped MX dequant back to packed rows y[total_M, *].  colwise = 0: q[R, C]
+ * holds each group's rows at padded offsets (group_offs_padded), e8m0[R, C/32];
+ * y is [total_M, C].  colwise = 1: q[R, C] is the transposed colwise copy
+ * whose columns are the padded rows, e8m0[R, C/32]; y is [total_M, R].
+ * Packed row r of group g (group_offs[g] <= r < group_offs[g+1]) reads padded
+ * row r - group_offs[g] + group_offs_padded[g].  Offsets stay on the device.
+ * Replaces grouped_dequantize_mxfp8 (csrc/pytorch/quantization/quantization.cpp:360-425). */
+int pta_grouped_dequantize_mxfp8(const void *q, int fmt, int64_t R, int64_t C, const uint8_t *e8m0,
+                                 int colwise, const int64_t *group_offs,
+                                 const int64_t *group_offs_padded, int64_t G, int64_t total_M,
+                                 void *y, int out_dtype, pta_stream_t stream);
+
 /* ============================================================================
  * Layout helpers
  * ========================================================================== */

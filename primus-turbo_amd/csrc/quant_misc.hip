@@ -417,7 +417,9 @@ template <int OUT_DT> __device__ __forceinline__ void store_out(void *y, int64_t
     else reinterpret_cast<uint16_t *>(y)[i] = f32_to_f16_bits(v);
 }
 
-// mode: 0 tensor, 1 rowwise [outer,len,inner], 2 block axis0, 3 block axis1, 4 block 2d, 5 mx
+// mode: 0 tensor, 1 rowwise [outer,len,inner], 2 block axis0, 3 block axis1, 4 block 2d, 5 mx,
+// 6 grouped mx rowwise (padded rows -> packed rows), 7 grouped mx colwise (transposed padded
+// columns -> packed rows)
 struct DQArgs {
     const uint8_t *q;
     const float   *s;
@@ -427,7 +429,20 @@ struct DQArgs {
     int64_t        d0, d1, d2; // mode-specific dims
     int64_t        block;
     int            transpose_out;
+    const int64_t *goffs, *goffs_pad; // grouped modes: [G+1] true / padded row offsets
+    int64_t        G;
 };
+
+// group of packed row r: the g with goffs[g] <= r < goffs[g+1] (binary search)
+__device__ __forceinline__ int64_t find_group(const int64_t *offs, int64_t G, int64_t r) {
+    int64_t lo = 0, hi = G; // invariant: offs[lo] <= r < offs[hi]
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (offs[mid] <= r) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
 
 template <int FMT, int OUT_DT, int MODE>
 __global__ __launch_bounds__(NT) void dequant_kernel(DQArgs a) {
@@ -451,10 +466,27 @@ __global__ __launch_bounds__(NT) void dequant_kernel(DQArgs a) {
             const int64_t mb = (M + a.block - 1) / a.block, nb = (N + a.block - 1) / a.block;
             const int64_t b = i / (M * N), r = (i / N) % M, c = i % N;
             sc = a.s[(b * mb + r / a.block) * nb + c / a.block];
-        } else { // MX: q[R, C], e[R, C/32]
+        } else if constexpr (MODE == 5) { // MX: q[R, C], e[R, C/32]
             const int64_t C = a.d1;
             const int64_t r = i / C, c = i % C;
             sc = __uint_as_float(static_cast<uint32_t>(a.e[r * (C / 32) + c / 32]) << 23);
+        }
+        if constexpr (MODE == 6) { // y[total_M, C] from q[padded rows, C], e[padded rows, C/32]
+            const int64_t C = a.d1;
+            const int64_t r = i / C, c = i % C;
+            const int64_t g  = find_group(a.goffs, a.G, r);
+            const int64_t sr = r - a.goffs[g] + a.goffs_pad[g];
+            sc = __uint_as_float(static_cast<uint32_t>(a.e[sr * (C / 32) + c / 32]) << 23);
+            store_out<OUT_DT>(a.y, i, fp8_to_f32<FMT>(a.q[sr * C + c]) * sc);
+            continue;
+        } else if constexpr (MODE == 7) { // y[total_M, R] from q[R, Cq] (columns padded per group)
+            const int64_t R = a.d0, Cq = a.d1;
+            const int64_t m = i / R, n = i % R;
+            const int64_t g  = find_group(a.goffs, a.G, m);
+            const int64_t sc_col = m - a.goffs[g] + a.goffs_pad[g];
+            sc = __uint_as_float(static_cast<uint32_t>(a.e[n * (Cq / 32) + sc_col / 32]) << 23);
+            store_out<OUT_DT>(a.y, i, fp8_to_f32<FMT>(a.q[n * Cq + sc_col]) * sc);
+            continue;
         }
         const float v = fp8_to_f32<FMT>(a.q[i]) * sc;
         if constexpr (MODE == 5) {
@@ -785,6 +817,24 @@ extern "C" int pta_dequantize_mxfp8(const void *q, int fmt, int64_t R, int64_t C
     a.q = static_cast<const uint8_t *>(q); a.e = e8m0; a.y = y;
     a.n = R * C; a.d0 = R; a.d1 = C; a.transpose_out = transpose_out;
     return launch_dequant<5>(a, fmt, out_dtype, as_stream(stream));
+}
+
+extern "C" int pta_grouped_dequantize_mxfp8(const void *q, int fmt, int64_t R, int64_t C,
+                                            const uint8_t *e8m0, int colwise, const int64_t *group_offs,
+                                            const int64_t *group_offs_padded, int64_t G, int64_t total_M,
+                                            void *y, int out_dtype, pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(q && y && e8m0 && group_offs && group_offs_padded, "pointers must be set");
+    PTA_CHECK_ARG(R >= 0 && C >= 0 && C % 32 == 0 && G >= 1 && total_M >= 0, "bad shape");
+    DQArgs a{};
+    a.q = static_cast<const uint8_t *>(q); a.e = e8m0; a.y = y;
+    a.d0 = R; a.d1 = C; a.goffs = group_offs; a.goffs_pad = group_offs_padded; a.G = G;
+    if (!colwise) {
+        a.n = total_M * C;
+        return launch_dequant<6>(a, fmt, out_dtype, as_stream(stream));
+    }
+    a.n = total_M * R;
+    return launch_dequant<7>(a, fmt, out_dtype, as_stream(stream));
 }
 
 extern "C" int pta_transpose_u8(const void *x, int64_t B, int64_t M, int64_t N, void *y,

@@ -430,6 +430,41 @@ def dequantize_mxfp8_impl(
     return y
 
 
+def grouped_dequantize_mxfp8_impl(
+    x: torch.Tensor,
+    out_dtype: torch.dtype,
+    axis: int,
+    block_size: int,
+    scale_inv: torch.Tensor,
+    group_offs: torch.Tensor,
+    group_offs_padded: torch.Tensor,
+    total_M: Optional[int] = None,
+) -> torch.Tensor:
+    """Grouped MX dequantize back to packed rows (quantization_impl.py:727-754):
+    axis 1 (rowwise, x = [padded rows, N_pad]) gives [total_M, N_pad]; axis 0
+    (colwise, x = the transposed copy [N, padded rows]) gives [total_M, N]."""
+    assert x.is_contiguous(), "The x tensor must be contiguous."
+    assert x.dim() == 2, "The x must be 2D tensor."
+    assert scale_inv.dim() == 2, "The scale_inv must be 2D tensor."
+    assert scale_inv.is_contiguous(), "The scale_inv tensor must be contiguous."
+    assert axis in (0, 1), "The axis must be 0 or 1."
+    assert out_dtype in (torch.float16, torch.bfloat16, torch.float32), f"unsupported out dtype {out_dtype}"
+    R, C = x.shape
+    assert C % block_size == 0, "The last dimension of the x tensor must be divisible by the block size."
+    G = group_offs.numel() - 1
+    assert G >= 1 and group_offs_padded.numel() == group_offs.numel()
+    if total_M is None:
+        total_M = int(group_offs[-1].item())
+    y = torch.empty((total_M, C if axis == 1 else R), dtype=out_dtype, device=x.device)
+    _C.call(
+        "pta_grouped_dequantize_mxfp8", _C.ptr(x), _C.fp8_code(x.dtype), R, C,
+        _C.ptr(scale_inv.view(torch.uint8)), int(axis == 0), _C.ptr(group_offs.contiguous()),
+        _C.ptr(group_offs_padded.contiguous()), G, total_M, _C.ptr(y), _C.out_dtype_code(out_dtype),
+        _C.stream(x.device),
+    )
+    return y
+
+
 def transpose_fp8(x: torch.Tensor) -> torch.Tensor:
     """Byte transpose of the last two dims of a 2D / 3D fp8 tensor."""
     x = x.contiguous()

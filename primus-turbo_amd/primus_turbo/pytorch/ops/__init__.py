@@ -2,6 +2,7 @@ from primus_turbo.pytorch.ops.gemm_fp8 import gemm_fp8  # noqa: F401
 from primus_turbo.pytorch.ops.grouped_gemm_fp8 import grouped_gemm_fp8  # noqa: F401
 from primus_turbo.pytorch.ops.quantization import (  # noqa: F401
     dequantize_fp8,
+    grouped_dequantize_fp8,
     grouped_quantize_fp8,
     grouped_quantize_fp8_with_trans,
     quantize_fp8,

@@ -18,6 +18,7 @@ from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
     dequantize_fp8_rowwise_impl,
     dequantize_fp8_tensorwise_impl,
     dequantize_mxfp8_impl,
+    grouped_dequantize_mxfp8_impl,
     grouped_quantize_mxfp8_impl,
     quant_fp8_blockwise_dual_impl,
     quant_fp8_blockwise_for_weight_impl,
@@ -33,6 +34,7 @@ __all__ = [
     "dequantize_fp8",
     "grouped_quantize_fp8",
     "grouped_quantize_fp8_with_trans",
+    "grouped_dequantize_fp8",
 ]
 
 
@@ -158,3 +160,25 @@ def dequantize_fp8(
         return dequantize_mxfp8_impl(x, out_dtype, axis, block_size, scale_inv)
     else:
         raise NotImplementedError(f"Unknown granularity {granularity}")
+
+
+def grouped_dequantize_fp8(
+    x: torch.Tensor,
+    out_dtype: torch.dtype,
+    granularity: ScalingGranularity,
+    group_offs: torch.Tensor,
+    group_offs_padded: torch.Tensor,
+    *,
+    block_size: Optional[int] = None,
+    axis: Optional[int] = None,
+    scale_inv: torch.Tensor,
+    scaling_recipe: Optional[ScalingRecipe] = None,
+    total_M: Optional[int] = None,
+) -> torch.Tensor:
+    """Grouped FP8 dequantize (ops/quantization.py:272-296): MX_BLOCKWISE only."""
+    if granularity == ScalingGranularity.MX_BLOCKWISE:
+        assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
+        return grouped_dequantize_mxfp8_impl(
+            x, out_dtype, axis, block_size, scale_inv, group_offs, group_offs_padded, total_M
+        )
+    raise NotImplementedError(f"Unknown granularity {granularity}")

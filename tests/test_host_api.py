@@ -87,3 +87,64 @@ def test_float8_linear_conversion():
     assert same is lin and isinstance(lin, turbo.modules.Float8Linear)
     assert lin.config.granularity == ScalingGranularity.TENSORWISE
     assert "config=" in repr(lin)
+
+
+def _qt_host(shape, data_shape, gran, scale, **kw):
+    from primus_turbo.pytorch.core.quantized_tensor import QuantizedTensor
+
+    g = torch.Generator().manual_seed(3)
+    data = torch.randint(0, 120, data_shape, dtype=torch.uint8, generator=g).view(torch.float8_e4m3fn)
+    return QuantizedTensor(data, scale, shape=torch.Size(shape), orig_dtype=torch.bfloat16,
+                           dest_dtype=torch.float8_e4m3fn, granularity=gran, **kw)
+
+
+def test_quantized_tensor_is_a_tensor_wrapper():
+    """QuantizedTensor behaves as the reference's wrapper subclass: outer
+    shape / dtype of the high-precision tensor, views without dequantizing
+    (quantized_tensor.py:148-836)."""
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity as SG
+    from primus_turbo.pytorch.core.quantized_tensor import QuantizedTensor
+
+    qt = _qt_host((64, 256), (64, 256), SG.TENSORWISE, torch.ones(()))
+    assert isinstance(qt, torch.Tensor) and isinstance(qt, QuantizedTensor)
+    assert qt.shape == (64, 256) and qt.dtype == torch.bfloat16 and qt.real_dtype == torch.float8_e4m3fn
+    assert qt.dim() == 2 and qt.size(-1) == 256 and qt.device.type == "cpu"
+    v = qt.view(32, 512)
+    assert isinstance(v, QuantizedTensor) and v.shape == (32, 512)
+    assert v.qdata.shape == (32, 512) and v.qdata.data_ptr() == qt.qdata.data_ptr()
+    r = qt.reshape(-1, 128)
+    assert r.shape == (128, 128) and r.qdata.shape == (128, 128)
+    d = qt.detach()
+    assert isinstance(d, QuantizedTensor) and d.granularity == SG.TENSORWISE and not d.requires_grad
+    row = qt[3]
+    assert not isinstance(row, QuantizedTensor) and torch.equal(row.view(torch.uint8), qt.qdata[3].view(torch.uint8))
+    names, meta = qt.__tensor_flatten__()
+    back = QuantizedTensor.__tensor_unflatten__({n: getattr(qt, n) for n in names}, meta, qt.shape, qt.stride())
+    assert back.shape == qt.shape and back.granularity == qt.granularity and back.qdata is qt.qdata
+    with pytest.raises(NotImplementedError):
+        qt + 1  # arithmetic is not defined on quantized data
+
+
+def test_quantized_tensor_mx_view_keeps_padding():
+    """MX data is stored with the inner dim padded to 128 and one exponent per
+    32 elements; a view re-pads the target shape the same way."""
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity as SG, ScalingRecipe
+    from primus_turbo.pytorch.core.quantized_tensor import QuantizedTensor
+
+    e = torch.zeros((64, 4), dtype=torch.uint8)
+    qt = _qt_host((64, 100), (64, 128), SG.MX_BLOCKWISE, e, block_size=32, scaling_recipe=ScalingRecipe(),
+                  quantized_axis=-1)
+    v = qt.view(32, 200)
+    assert v.shape == (32, 200) and v.qdata.shape == (32, 256) and v.scale_inv.shape == (32, 8)
+    assert v.quantized_axis == 1
+
+
+def test_quantized_tensor_view_autograd():
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity as SG
+
+    qt = _qt_host((64, 256), (64, 256), SG.TENSORWISE, torch.ones(()), requires_grad=True)
+    v = qt.view(128, 128)
+    assert v.requires_grad
+    g = torch.ones((128, 128), dtype=torch.bfloat16)
+    (gin,) = torch.autograd.grad(v, qt, g)
+    assert gin.shape == (64, 256)
