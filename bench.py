@@ -259,6 +259,7 @@ def _other_configs(args):
         quantize_fp8_tensorwise_impl,
         quantize_mxfp8_impl,
     )
+    from primus_turbo.pytorch.ops.gemm_fp8 import _mx_strides
 
     SG = ScalingGranularity
     dev = "cuda:0"
@@ -330,13 +331,17 @@ def _other_configs(args):
     sign = lambda t: torch.where(torch.rand(t, generator=g) < 0.5, -1.0, 1.0)  # noqa: E731
     a5 = (sign((8192, 8192)) * torch.exp(torch.randn((8192, 8192), generator=g) * 1.5)).bfloat16().to(dev)
     w5 = (sign((28672, 8192)) * torch.exp(torch.randn((28672, 8192), generator=g) * 1.5)).bfloat16().to(dev)
-    qa5, ea5 = quantize_mxfp8_impl(a5, e4, 1, 32)
-    qw5, ew5 = quantize_mxfp8_impl(w5, e4, 1, 32)
+    # the layout gemm_fp8's MX forward uses: exponents K-block major
+    qa5, ea5 = quantize_mxfp8_impl(a5, e4, 1, 32, exp_kmajor=True)
+    qw5, ew5 = quantize_mxfp8_impl(w5, e4, 1, 32, exp_kmajor=True)
+    o5 = torch.empty((8192, 28672), dtype=torch.bfloat16, device=dev)
     res["cfg5_mxfp8_8192x28672x8192_NT"] = {
-        "quant_dual_A": _quant_rec(_time_cuda(lambda: quantize_mxfp8_impl(a5, e4, None, 32, with_trans=True), it, 2),
+        "quant_dual_A": _quant_rec(_time_cuda(lambda: quantize_mxfp8_impl(a5, e4, None, 32, with_trans=True,
+                                                                          exp_kmajor=True), it, 2),
                                    a5.numel() * (2 + 1 + 1) + 2 * a5.numel() // 32),
-        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_impl(qa5, ea5, False, qw5, ew5, True, torch.bfloat16, False,
-                                                           SG.MX_BLOCKWISE.value), it, 2), 2.0 * 8192 * 28672 * 8192),
+        "gemm": _gemm_rec(_time_cuda(lambda: gemm_fp8_nt(qa5, qw5, torch.bfloat16, SG.MX_BLOCKWISE, ea5,
+                                                         _mx_strides(ea5), False, ew5, _mx_strides(ew5), False,
+                                                         out=o5), it, 2), 2.0 * 8192 * 28672 * 8192),
     }
     return res
 

@@ -128,14 +128,22 @@ int pta_quantize_fp8_blockwise_segment_m_row_col(const void *x, int in_dtype, in
                                                  float *s_col_pad, int64_t *vk_lens,
                                                  int64_t *vk_offs, int fmt, pta_stream_t stream);
 
+/* Exponent layout of pta_quantize_mxfp8: 0 = [rows, cols_pad/32] (the
+ * reference's); PTA_MX_EXP_KMAJOR = K-block major [cols_pad/128][rows][4]: the
+ * four exponents of one 128-column block of a row are one dword and the
+ * dwords of consecutive rows are contiguous (a GEMM staging the exponents of
+ * one K block for 64 rows then reads 256 contiguous bytes). */
+#define PTA_MX_EXP_KMAJOR 1
+
 /* MXFP8 (block 32, E8M0): x[G, M, N].  Rowwise output q_row[G*M, N_pad],
  * e_row[G*M, N_pad/32]; colwise output (transposed) q_col[G*N, M_pad],
  * e_col[G*N, M_pad/32]; pads are 128 and padded elements are 0.  Either pair
- * may be NULL.  use_2d_* shares one exponent per 32 x 32 tile.
+ * may be NULL.  use_2d_* shares one exponent per 32 x 32 tile.  `layout`
+ * selects the exponent layout (0 or PTA_MX_EXP_KMAJOR).
  * Replaces quantize_mxfp8 / quantize_mxfp8_dual (quantization.cpp:736-967). */
 int pta_quantize_mxfp8(const void *x, int in_dtype, int64_t G, int64_t M, int64_t N, void *q_row,
                        uint8_t *e_row, int use_2d_row, void *q_col, uint8_t *e_col, int use_2d_col,
-                       int fmt, pta_stream_t stream);
+                       int fmt, int layout, pta_stream_t stream);
 
 /* Grouped MXFP8 (block 32, E8M0) of x[M, N] whose rows are split into G
  * groups by group_offs[G+1] (device).  Each group is zero-padded along M to
@@ -249,7 +257,10 @@ int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int trans_a, con
  * strides and explicit scale addressing.  Blockwise scales are read as
  * a_scale[r * sa_m + kb * sa_k] with r = m (or m / 128 when a_scale_2d) and
  * kb = k / 128; likewise for B.  MX scales are e8m0 bytes at
- * a_scale[m * sa_m + k / 32].  *_scale_bytes bound the scale arrays.  This has
+ * a_scale[m * sa_m + (k / 128) * sa_k + (k / 32) % 4] (row-major
+ * [rows, K/32]: sa_m = K/32, sa_k = 4, where sa_k = 0 is read as 4;
+ * PTA_MX_EXP_KMAJOR: sa_m = 4, sa_k = 4 * rows); sa_m and sa_k must be
+ * multiples of 4.  *_scale_bytes bound the scale arrays.  This has
  * no single counterpart in the reference; it is the kernel interface below
  * gemm_fp8_impl that the autograd functions use to consume transposed
  * quantized copies without extra layout passes. */

@@ -14,6 +14,10 @@ int gemm_nt_launch(const uint8_t *a, int fa, int64_t lda, const uint8_t *b, int 
     g.a = a; g.b = b; g.c = c; g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
     g.sa = sa; g.sb = sb; g.sa_m = sa_m; g.sa_k = sa_k; g.sb_m = sb_m; g.sb_k = sb_k;
     g.sa_bytes = sa_bytes; g.sb_bytes = sb_bytes;
+    if (sm == SM_MX) { // row-major exponents unless a K-block stride is given
+        if (g.sa_k == 0) g.sa_k = 4;
+        if (g.sb_k == 0) g.sb_k = 4;
+    }
     g.tiles_m = static_cast<int>(cdiv(M, BM));
     g.tiles_n = static_cast<int>(cdiv(N, BN));
     g.group_m = 4;
@@ -106,7 +110,7 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
         else if (!trans_a) { b2d = true; sb_m = 1; sb_k = cdiv(N, 128); } // NN: [K/128, N/128]
         else { b2d = false; sb_m = 1; sb_k = N; }                         // TN: [K/128, N]
     } else if (sm == SM_MX) {
-        sa_m = K / 32; sb_m = K / 32;
+        sa_m = K / 32; sb_m = K / 32; sa_k = 4; sb_k = 4;
     }
     // extent of each scale array in bytes
     int64_t sa_bytes = 4, sb_bytes = 4;
@@ -143,6 +147,16 @@ extern "C" int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, co
     PTA_CHECK_ARG(K % 16 == 0 && lda % 16 == 0 && ldb % 16 == 0, "K and row strides must be multiples of 16");
     PTA_CHECK_ARG(aligned16(a) && aligned16(b), "A and B must be 16-byte aligned");
     PTA_CHECK_ARG(!(a_scale_2d && b_scale_2d), "2-D scales on both operands are not supported");
+    if (sm == SM_MX) {
+        PTA_CHECK_ARG(K % 128 == 0, "MX_BLOCKWISE needs K %% 128 == 0");
+        PTA_CHECK_ARG(sa_m % 4 == 0 && sa_k % 4 == 0 && sb_m % 4 == 0 && sb_k % 4 == 0 && sa_m >= 0 &&
+                          sa_k >= 0 && sb_m >= 0 && sb_k >= 0,
+                      "MX exponent strides must be non-negative multiples of 4");
+        const int64_t nkb = K / 128, ska = sa_k ? sa_k : 4, skb = sb_k ? sb_k : 4;
+        PTA_CHECK_ARG(M == 0 || N == 0 || ((M - 1) * sa_m + (nkb - 1) * ska + 4 <= a_scale_bytes &&
+                                           (N - 1) * sb_m + (nkb - 1) * skb + 4 <= b_scale_bytes),
+                      "MX exponent arrays are smaller than the strides address");
+    }
     if (M == 0 || N == 0 || K == 0) {
         PTA_CHECK_ARG(K != 0 || M == 0 || N == 0, "K == 0 is not supported by the strided entry");
         return PTA_OK;

@@ -281,6 +281,7 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
                           __builtin_amdgcn_readfirstlane(dMX0.z), __builtin_amdgcn_readfirstlane(dMX0.w)};
     const int mx_vo = wave < 4 ? static_cast<int>((m0 + 64 * wave + lane) * g.sa_m)
                                : static_cast<int>((n0 + 64 * (wave - 4) + lane) * g.sb_m);
+    const int mx_ks = static_cast<int>(wave < 4 ? g.sa_k : g.sb_k); // exponent bytes per K block
     auto issue = [&](int kb, int stage) {
         const int      k0 = kb * BK;
         const uint32_t la = lds0 + stage * STAGE_ + wave * RPW_A * BK;
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
             // rows each, waves 4..7 64 B rows each
             if (wave < 4 + BN_ / 64)
                 dma4(lds0 + SBASE_ + stage * SSLOT_ + wave * 256, mx_vo, dMX,
-                     static_cast<int>(kb + kb_base) * 4);
+                     static_cast<int>(kb + kb_base) * mx_ks);
         }
     };
 

@@ -148,7 +148,7 @@ extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scal
     } else if (sm == SM_ROW) {
         g.sa_bytes = M_total * 4; g.sb_bytes = N * 4; g.sb_gstride = N * 4; // b_scale [G, N]
     } else if (sm == SM_MX) {
-        g.sa_m = K / 32; g.sb_m = K / 32; g.sa_bytes = M_total * (K / 32);
+        g.sa_m = K / 32; g.sb_m = K / 32; g.sa_k = 4; g.sb_k = 4; g.sa_bytes = M_total * (K / 32);
         g.sb_gstride = N * (K / 32); g.sb_bytes = g.sb_gstride;
     } else {
         g.sa_bytes = 4; g.sb_bytes = 4; g.sb_gstride = 0; // one scalar shared by all groups
@@ -260,7 +260,7 @@ extern "C" int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt
     g.M = swap ? OUT_N : OUT_M; g.N = swap ? OUT_M : OUT_N; g.K = K_pad;
     g.lda = K_pad; g.ldb = K_pad; g.ldc = g.N;
     g.sa = swap ? rhs_scale : lhs_scale; g.sb = swap ? lhs_scale : rhs_scale;
-    g.sa_m = K_pad / 32; g.sb_m = K_pad / 32;
+    g.sa_m = K_pad / 32; g.sb_m = K_pad / 32; g.sa_k = 4; g.sb_k = 4;
     g.sa_bytes = g.M * (K_pad / 32); g.sb_bytes = g.N * (K_pad / 32);
     g.group_mode = 2; g.group_offs = group_offs; g.G = G;
     g.c = out; g.c_gstride = OUT_M * OUT_N * static_cast<int64_t>(eb);

@@ -267,6 +267,10 @@ struct MXArgs {
     int64_t     M, N, M_pad, N_pad;
     uint8_t    *q_row, *e_row, *q_col, *e_col;
     int         use2d_row, use2d_col, vec;
+    // exponent layout: 0 = [rows, cols/32]; 1 = K-block major [cols/128][rows][4]
+    // with erows_row / erows_col rows in the rowwise / colwise arrays
+    int         ekmaj;
+    int64_t     erows_row, erows_col;
     // grouped rows (x[M, N] split by goffs[G+1]): tiles live in the 128-padded
     // colwise space offs_col; the rowwise output places group g at offs_row[g]
     const int64_t *goffs, *offs_row, *offs_col;
@@ -348,8 +352,11 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         blk = max_xor32(max_xor16(blk));
     }
 
+    // The tile's exponents are staged in LDS and stored as one dword per row
+    // (rowwise: the tile's 4 column blocks; colwise: its 4 row blocks):
+    // scattered single-byte stores cost a third of the kernel's time.
+    __shared__ uint32_t s_exp[2][128];
     if constexpr (ROW) {
-        const int64_t eb_row = a.N_pad / 32;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int lr = rgrp * 4 + i;
@@ -360,7 +367,7 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             uint8_t      *dst  = a.q_row + orow * a.N_pad + n0;
             *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(&v[i][0], sc), quant4<FMT>(&v[i][4], sc),
                                                          quant4<FMT>(&v[i][8], sc), quant4<FMT>(&v[i][12], sc));
-            if ((cseg & 1) == 0) a.e_row[orow * eb_row + n0 / 32] = static_cast<uint8_t>(e);
+            if ((cseg & 1) == 0) reinterpret_cast<uint8_t *>(&s_exp[0][lr])[cseg >> 1] = static_cast<uint8_t>(e);
         }
     }
 
@@ -383,10 +390,14 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             for (int i = 0; i < 4; ++i)
                 packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(v[i][j], sc))) << (8 * i);
             s_tr[cseg * 16 + j][rgrp] = packed;
-            const int64_t n = n0 + j;
-            if ((rgrp & 7) == 0 && n < N) a.e_col[(g * N + n) * eb_col + tm * 4 + wave] = static_cast<uint8_t>(e);
+            if ((rgrp & 7) == 0) reinterpret_cast<uint8_t *>(&s_exp[1][cseg * 16 + j])[wave] = static_cast<uint8_t>(e);
         }
         __syncthreads();
+        if (t < 128 && tn * 128 + t < N) {
+            const int64_t n = g * N + tn * 128 + t;
+            uint8_t *d = a.ekmaj ? a.e_col + (tm * a.erows_col + n) * 4 : a.e_col + n * eb_col + tm * 4;
+            *reinterpret_cast<uint32_t *>(d) = s_exp[1][t];
+        }
         // 128 output rows (n) x 128 bytes (m) in 16-byte chunks
 #pragma unroll
         for (int it = 0; it < 4; ++it) {
@@ -398,6 +409,15 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             const uint32_t *src = &s_tr[nl][mc >> 2];
             *reinterpret_cast<uint4 *>(a.q_col + (g * N + n) * a.M_pad + tm * 128 + mc) =
                 make_uint4(src[0], src[1], src[2], src[3]);
+        }
+    }
+    if constexpr (ROW) {
+        if constexpr (!COL) __syncthreads();
+        // exponent bytes of the tile's 4 column blocks, one dword per output row
+        if (t < 128 && t < nout) {
+            const int64_t r = orow0 + t;
+            uint8_t *d = a.ekmaj ? a.e_row + (tn * a.erows_row + r) * 4 : a.e_row + r * (a.N_pad / 32) + tn * 4;
+            *reinterpret_cast<uint32_t *>(d) = s_exp[0][t];
         }
     }
 }
@@ -632,13 +652,15 @@ int check_in(const void *x, int in_dtype, int fmt) {
 
 template <int IN_DT, int FMT>
 int mx_launch(const void *x, int64_t G, int64_t M, int64_t N, uint8_t *q_row, uint8_t *e_row,
-              int u2r, uint8_t *q_col, uint8_t *e_col, int u2c, hipStream_t st) {
+              int u2r, uint8_t *q_col, uint8_t *e_col, int u2c, int layout, hipStream_t st) {
     MXArgs a{};
     a.x = x; a.M = M; a.N = N;
     a.M_pad = cdiv(M, 128) * 128;
     a.N_pad = cdiv(N, 128) * 128;
     a.q_row = q_row; a.e_row = e_row; a.q_col = q_col; a.e_col = e_col;
     a.use2d_row = u2r; a.use2d_col = u2c;
+    a.ekmaj = layout == PTA_MX_EXP_KMAJOR;
+    a.erows_row = G * M; a.erows_col = G * N;
     a.vec = aligned16(x) ? 1 : 0;
     const dim3 grid(static_cast<uint32_t>(a.M_pad / 128), static_cast<uint32_t>(a.N_pad / 128),
                     static_cast<uint32_t>(G));
@@ -732,7 +754,7 @@ extern "C" int pta_quantize_fp8_rowwise(const void *x, int in_dtype, int64_t out
 
 extern "C" int pta_quantize_mxfp8(const void *x, int in_dtype, int64_t G, int64_t M, int64_t N,
                                   void *q_row, uint8_t *e_row, int use_2d_row, void *q_col,
-                                  uint8_t *e_col, int use_2d_col, int fmt, pta_stream_t stream) {
+                                  uint8_t *e_col, int use_2d_col, int fmt, int layout, pta_stream_t stream) {
     clear_error();
     if (int rc = check_in(x, in_dtype, fmt)) return rc;
     PTA_CHECK_ARG(in_dtype != PTA_F32, "MXFP8 quantization takes bf16 or fp16 input");
@@ -741,11 +763,12 @@ extern "C" int pta_quantize_mxfp8(const void *x, int in_dtype, int64_t G, int64_
     PTA_CHECK_ARG((q_row == nullptr) == (e_row == nullptr), "q_row/e_row must both be set or NULL");
     PTA_CHECK_ARG((q_col == nullptr) == (e_col == nullptr), "q_col/e_col must both be set or NULL");
     PTA_CHECK_ARG(q_row || q_col, "no output requested");
+    PTA_CHECK_ARG(layout == 0 || layout == PTA_MX_EXP_KMAJOR, "unknown exponent layout %d", layout);
     PTA_CHECK_ARG((!q_row || aligned16(q_row)) && (!q_col || aligned16(q_col)), "outputs must be 16-byte aligned");
     if (M == 0 || N == 0) return PTA_OK;
     return PTA_DISPATCH_IN_FMT(in_dtype, fmt, mx_launch, x, G, M, N, static_cast<uint8_t *>(q_row),
                                e_row, use_2d_row, static_cast<uint8_t *>(q_col), e_col, use_2d_col,
-                               as_stream(stream));
+                               layout, as_stream(stream));
 }
 
 extern "C" int pta_grouped_quantize_mxfp8(const void *x, int in_dtype, int64_t M, int64_t N, int64_t G,

@@ -19,6 +19,8 @@ PTA_E4M3, PTA_E5M2 = 0, 1
 PTA_TENSORWISE, PTA_ROWWISE, PTA_BLOCKWISE, PTA_MX_BLOCKWISE = 1, 2, 3, 4
 # layout flags of pta_quantize_fp8_blockwise_dual
 DUAL_COL_TRANSPOSED, DUAL_ROW_SCALE_KMAJOR = 1, 2
+# exponent layout flag of pta_quantize_mxfp8
+MX_EXP_KMAJOR = 1
 
 _vp, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
 
@@ -37,7 +39,7 @@ SIGNATURES = {
         _i32,
         [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp],
     ),
-    "pta_quantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp]),
+    "pta_quantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "pta_dequantize_fp8_tensorwise": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp]),
     "pta_dequantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp]),
     "pta_dequantize_fp8_blockwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),

@@ -281,7 +281,16 @@ def quantize_mxfp8_impl(
     with_trans: bool = False,
     scaling_recipe: Optional[ScalingRecipe] = None,
     scaling_recipe_for_trans: Optional[ScalingRecipe] = None,
+    exp_kmajor: bool = False,
 ):
+    """MXFP8 quantization (quantization_impl.py:489-543 in the reference).
+
+    ``exp_kmajor=True`` (an extension used by the autograd function) returns
+    each exponent array as its ``[cols_pad/128, rows, 4]`` K-block-major
+    storage (``PTA_MX_EXP_KMAJOR``) instead of ``[rows, cols_pad/32]``: the
+    kernel then writes one 512-byte run per 128x128 tile and the GEMM reads
+    the exponents of one K block for 64 rows from 256 contiguous bytes.
+    """
     _check_hp(x)
     assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
     assert x.dtype in (torch.bfloat16, torch.float16), "Input must be BFloat16 or Half"
@@ -311,17 +320,19 @@ def quantize_mxfp8_impl(
     q_row = e_row = q_col = e_col = None
     if row:
         q_row = torch.empty((G * M, Np), dtype=out_dtype, device=dev)
-        e_row = torch.empty((G * M, Np // 32), dtype=torch.uint8, device=dev)
+        e_row = torch.empty((Np // 128, G * M, 4) if exp_kmajor else (G * M, Np // 32), dtype=torch.uint8, device=dev)
     if col:
         q_col = torch.empty((G * N, Mp), dtype=out_dtype, device=dev)
-        e_col = torch.empty((G * N, Mp // 32), dtype=torch.uint8, device=dev)
+        e_col = torch.empty((Mp // 128, G * N, 4) if exp_kmajor else (G * N, Mp // 32), dtype=torch.uint8, device=dev)
     _C.call(
         "pta_quantize_mxfp8", _C.ptr(x), _C.in_dtype_code(x.dtype), G, M, N, _C.ptr(q_row), _C.ptr(e_row),
         int(rr.use_2d_block), _C.ptr(q_col), _C.ptr(e_col), int(rc.use_2d_block), _C.fp8_code(out_dtype),
-        _C.stream(dev),
+        _C.MX_EXP_KMAJOR if exp_kmajor else 0, _C.stream(dev),
     )
 
     def shape3(t, rows):
+        if exp_kmajor and t.dtype == torch.uint8:
+            return t  # K-block-major exponent storage, returned as is
         return t.view(G, rows, -1) if x.dim() == 3 else t
 
     outs = []

@@ -11,7 +11,7 @@ runs NT.  The arithmetic (which bytes, which scales, fp32 accumulation per
 
 from __future__ import annotations
 
-from typing import Optional, Union
+from typing import Optional, Tuple, Union
 
 import torch
 
@@ -33,9 +33,9 @@ from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_impl, gemm_
 from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
     quant_fp8_blockwise_dual_impl,
     quant_fp8_blockwise_for_weight_impl,
+    quantize_mxfp8_impl,
     transpose_fp8,
 )
-from primus_turbo.pytorch.ops.quantization import quantize_fp8_with_trans
 
 __all__ = ["gemm_fp8"]
 
@@ -262,11 +262,19 @@ class FP8GemmBlockFunction(torch.autograd.Function):
 # ===========================================================================
 # MX_BLOCKWISE (gemm_fp8.py:509-647): NT only, E8M0 per 32-K block.
 # ===========================================================================
+def _mx_strides(e: torch.Tensor) -> Tuple[int, int]:
+    """(row stride, K-block stride) in bytes of an exponent array: K-block
+    major ``[K/128, rows, 4]`` storage or the reference's ``[rows, K/32]``."""
+    if e.dim() == 3:
+        return 4, 4 * e.shape[1]
+    return e.shape[-1], 4
+
+
 def _mx_gemm(a_q, a_e, b_q, b_e, out_dtype):
     K = a_q.shape[1]
     assert b_q.shape[1] == K
-    return gemm_fp8_nt(a_q, b_q, out_dtype, ScalingGranularity.MX_BLOCKWISE, a_e, (K // 32, 0), False,
-                       b_e, (K // 32, 0), False)
+    return gemm_fp8_nt(a_q, b_q, out_dtype, ScalingGranularity.MX_BLOCKWISE, a_e, _mx_strides(a_e), False,
+                       b_e, _mx_strides(b_e), False)
 
 
 class FP8GemmMXFunction(torch.autograd.Function):
@@ -286,8 +294,9 @@ class FP8GemmMXFunction(torch.autograd.Function):
                                                scaling_recipe=ra)
             a_col, a_col_s = a_t.qdata, a_t.scale_inv
         else:
-            a_row, a_row_s, a_col, a_col_s = quantize_fp8_with_trans(a.detach(), fdt, gran, block_size=bs,
-                                                                     scaling_recipe=ra)
+            a_row, a_row_s, a_col, a_col_s = quantize_mxfp8_impl(a.detach(), fdt, None, bs, with_trans=True,
+                                                                 scaling_recipe=ra, scaling_recipe_for_trans=ra,
+                                                                 exp_kmajor=True)
         rb = ScalingRecipe(use_2d_block=True)
         if isinstance(b, QuantizedTensor):
             check_quantized_tensor(b, config, axis=-1, scaling_recipe=rb)
@@ -297,8 +306,9 @@ class FP8GemmMXFunction(torch.autograd.Function):
                                                scaling_recipe=rb)
             b_col, b_col_s = b_t.qdata, b_t.scale_inv
         else:
-            b_row, b_row_s, b_col, b_col_s = quantize_fp8_with_trans(
-                b.detach(), fdt, gran, block_size=bs, scaling_recipe=rb, scaling_recipe_for_trans=rb
+            b_row, b_row_s, b_col, b_col_s = quantize_mxfp8_impl(
+                b.detach(), fdt, None, bs, with_trans=True, scaling_recipe=rb, scaling_recipe_for_trans=rb,
+                exp_kmajor=True,
             )
         out = _mx_gemm(a_row, a_row_s, b_row, b_row_s, out_dtype)
         ctx.save_for_backward(a_col, a_col_s, b_col, b_col_s)
@@ -311,8 +321,8 @@ class FP8GemmMXFunction(torch.autograd.Function):
         a_col, a_col_s, b_col, b_col_s = ctx.saved_tensors
         gdt = _get_fp8_dtype(ctx.config.format, False)
         grad_out = grad_out.reshape(grad_out.shape[0], -1).contiguous()
-        g_row, g_row_s, g_col, g_col_s = quantize_fp8_with_trans(
-            grad_out, gdt, ctx.config.granularity, block_size=ctx.config.block_size
+        g_row, g_row_s, g_col, g_col_s = quantize_mxfp8_impl(
+            grad_out, gdt, None, ctx.config.block_size, with_trans=True, exp_kmajor=True
         )
         grad_a = _mx_gemm(g_row, g_row_s, b_col, b_col_s, ctx.out_dtype)  # [M, K]
         grad_b = _mx_gemm(g_col, g_col_s, a_col, a_col_s, ctx.out_dtype)  # [N, K]

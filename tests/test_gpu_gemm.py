@@ -126,6 +126,15 @@ def test_gemm_mx_vs_oracle(mnk, fmts):
     out = gemm_fp8_impl(qa, ea, False, qb, eb, True, torch.bfloat16, False, g.value)
     ref = O.gemm_ref(da, db, False, True)
     _check(out, ref, "MX")
+    # the same operands with K-block-major exponents give the same output bits
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import quantize_mxfp8_impl
+    from primus_turbo.pytorch.ops.gemm_fp8 import _mx_strides
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_nt
+
+    qak, eak = quantize_mxfp8_impl(a.cuda(), fmts[0], 1, 32, scaling_recipe=SR(), exp_kmajor=True)
+    qbk, ebk = quantize_mxfp8_impl(b.cuda(), fmts[1], 1, 32, scaling_recipe=SR(use_2d_block=True), exp_kmajor=True)
+    outk = gemm_fp8_nt(qak, qbk, torch.bfloat16, g, eak, _mx_strides(eak), False, ebk, _mx_strides(ebk), False)
+    assert torch.equal(outk[:, :N], out), "k-major exponents change the MX GEMM result"
 
 
 def _autograd_case(m, n, k, layout, fmt_name, gran_name, block_size=None, dtype=torch.bfloat16):

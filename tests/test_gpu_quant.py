@@ -274,6 +274,18 @@ def test_mxfp8_vs_oracle(shape, qdt, use_2d):
                                                           scaling_recipe=r, scaling_recipe_for_trans=r)
         assert_bytes_equal(u8(qr), O.quant_mx(x, FMT[qdt], 1, use_2d)[0], "dual row bytes")
         assert_bytes_equal(u8(qc), O.quant_mx(x, FMT[qdt], 0, use_2d)[0], "dual col bytes")
+        # K-block-major exponents: same bytes, stored [cols_pad/128, rows, 4]
+        from primus_turbo.pytorch.kernels.quantization.quantization_impl import quantize_mxfp8_impl
+
+        qrk, erk, qck, eck = quantize_mxfp8_impl(x.cuda(), qdt, None, 32, with_trans=True, scaling_recipe=r,
+                                                 scaling_recipe_for_trans=r, exp_kmajor=True)
+        assert_bytes_equal(u8(qrk), u8(qr), "dual row bytes (k-major exponents)")
+        assert_bytes_equal(u8(qck), u8(qc), "dual col bytes (k-major exponents)")
+        for ek, e_ref, what in ((erk, er, "row"), (eck, ec, "col")):
+            nb, rows, four = ek.shape
+            assert four == 4 and rows == e_ref.shape[0] and nb * 4 == e_ref.shape[1]
+            back = u8(ek).transpose(1, 0, 2).reshape(rows, nb * 4)
+            assert_bytes_equal(back, u8(e_ref), f"k-major {what} exponents")
 
 
 # ---------------------------------------------------------------------------
