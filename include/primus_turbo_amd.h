@@ -206,6 +206,14 @@ int pta_grouped_dequantize_mxfp8(const void *q, int fmt, int64_t R, int64_t C, c
  * Layout helpers
  * ========================================================================== */
 
+/* E8M0 scale shuffle into the 16 x 16 MFMA layout: x[M, N] -> y[M_pad, N_pad],
+ * M_pad = roundup(M, 256), N_pad = roundup(N, 8), zero padded; 32 x 8 tiles,
+ * byte (16 h + r, 4 q + c) of a tile at offset 64 c + 4 r + 2 q + h.
+ * Replaces shuffle_scale(scale, [16, 16]) (csrc/kernels/shuffle/shuffle.cu:12-73,
+ * csrc/pytorch/shuffle/shuffle.cpp) and the shuffle_scale option of the MXFP8
+ * quantizers. */
+int pta_shuffle_e8m0_scale(const uint8_t *x, int64_t M, int64_t N, uint8_t *y, pta_stream_t stream);
+
 /* Byte transpose x[B, M, N] -> y[B, N, M].  Replaces transpose_2d
  * (csrc/pytorch/transpose/transpose.cpp) for fp8 tensors. */
 int pta_transpose_u8(const void *x, int64_t B, int64_t M, int64_t N, void *y, pta_stream_t stream);

@@ -276,6 +276,23 @@ def quant_mx_grouped(x, fmt, group_lens):
     return q_row, e_row, np.array(offs_row, np.int64), q_col, e_col, np.array(offs_col, np.int64)
 
 
+def shuffle_e8m0(e) -> np.ndarray:
+    """E8M0 16 x 16 MFMA scale shuffle (csrc/kernels/shuffle/shuffle.cu:12-73,
+    padding csrc/pytorch/shuffle/shuffle_meta.cpp:13-29): pad e[M, N] with zeros
+    to [roundup(M, 256), roundup(N, 8)], cut it into 32 x 8 tiles in row-major
+    tile order, and inside a tile write row 16*i1 + i2, column 4*i4 + i5 at
+    byte 64*i5 + 4*i2 + 2*i4 + i1 (the (i1, i2, i4, i5) -> (i5, i2, i4, i1)
+    index permutation of the reference's comment)."""
+    e = np.asarray(e, np.uint8)
+    M, N = e.shape
+    Mp, Np = -(-M // 256) * 256, -(-N // 8) * 8
+    p = np.zeros((Mp, Np), np.uint8)
+    p[:M, :N] = e
+    # [tile_row, i1, i2, tile_col, i4, i5] -> [tile_row, tile_col, i5, i2, i4, i1]
+    t = p.reshape(Mp // 32, 2, 16, Np // 8, 2, 4).transpose(0, 3, 5, 2, 4, 1)
+    return np.ascontiguousarray(t).reshape(Mp, Np)
+
+
 def mx_e8m0(amax: float, fmt: int) -> int:
     return int(lib().or_mx_e8m0(ctypes.c_float(amax), fmt))
 

@@ -13,6 +13,7 @@
 
 #include "primus_turbo/quantization.h"
 #include "primus_turbo/reduce.h"
+#include "primus_turbo/shuffle.h"
 
 using namespace primus_turbo;
 using bf16 = dtype::bfloat16;
@@ -120,6 +121,16 @@ int ref_quant_segment(const void *x, int64_t M, int64_t N, int64_t G, const int6
             reinterpret_cast<dtype::float8_e5m2 *>(q_col), s_row, s_col, group_offs, vk_offs, M, N, Mpad,
             static_cast<int>(G), fp8_max(fmt), st);
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// E8M0 scale shuffle of x[M, N] into y[roundup(M,256), roundup(N,8)] with the
+// reference's 16x16 layout (csrc/kernels/shuffle/shuffle.cu:12-73,125-139;
+// host padding as csrc/pytorch/shuffle/shuffle_meta.cpp:13-29).
+int ref_shuffle_e8m0(const void *x, int64_t M, int64_t N, void *y, void *stream) {
+    const int64_t Mp = (M + 255) / 256 * 256, Np = (N + 7) / 8 * 8;
+    shuffle_e8m0_scale(reinterpret_cast<uint8_t *>(const_cast<void *>(x)), reinterpret_cast<uint8_t *>(y), 16, 16,
+                       M, N, Mp, Np, reinterpret_cast<hipStream_t>(stream));
+    return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
 } // extern "C"

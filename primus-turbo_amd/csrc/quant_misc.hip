@@ -860,6 +860,39 @@ extern "C" int pta_grouped_dequantize_mxfp8(const void *q, int fmt, int64_t R, i
     return launch_dequant<7>(a, fmt, out_dtype, as_stream(stream));
 }
 
+// E8M0 scale shuffle (16 x 16 MFMA layout) of x[M, N] into y[M_pad, N_pad]
+// (M_pad = roundup(M, 256), N_pad = roundup(N, 8)): the padded array is cut
+// into 32 x 8 tiles stored one after another (row-major over tiles), and inside
+// a tile the byte of row 16*h + r, column 4*q + c goes to offset
+// 64*c + 4*r + 2*q + h.  One thread writes one output dword: the four bytes
+// of rows r, r + 16 and columns c, c + 4 of its tile; bytes outside x are 0.
+__global__ __launch_bounds__(NT) void shuffle_e8m0_kernel(const uint8_t *x, int64_t M, int64_t N, uint8_t *y,
+                                                          int64_t n_dwords, int64_t tiles_per_row) {
+    const int64_t d = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+    if (d >= n_dwords) return;
+    const int64_t tile = d >> 6;
+    const int     w    = static_cast<int>(d & 63);
+    const int     c = w >> 4, r = w & 15;
+    const int64_t row0 = (tile / tiles_per_row) * 32 + r, col0 = (tile % tiles_per_row) * 8 + c;
+    auto at = [&](int64_t rr, int64_t cc) -> uint32_t { return rr < M && cc < N ? x[rr * N + cc] : 0u; };
+    const uint32_t v = at(row0, col0) | (at(row0 + 16, col0) << 8) | (at(row0, col0 + 4) << 16) |
+                       (at(row0 + 16, col0 + 4) << 24);
+    reinterpret_cast<uint32_t *>(y)[d] = v;
+}
+
+extern "C" int pta_shuffle_e8m0_scale(const uint8_t *x, int64_t M, int64_t N, uint8_t *y, pta_stream_t stream) {
+    clear_error();
+    PTA_CHECK_ARG(x && y && M >= 0 && N >= 0, "bad arguments");
+    PTA_CHECK_ARG((reinterpret_cast<uintptr_t>(y) & 3) == 0, "output must be 4-byte aligned");
+    const int64_t Mp = cdiv(M, 256) * 256, Np = cdiv(N, 8) * 8;
+    const int64_t n_dwords = Mp * Np / 4;
+    if (n_dwords == 0) return PTA_OK;
+    shuffle_e8m0_kernel<<<static_cast<uint32_t>(cdiv(n_dwords, NT)), NT, 0, as_stream(stream)>>>(x, M, N, y, n_dwords,
+                                                                                                 Np / 8);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
+}
+
 extern "C" int pta_transpose_u8(const void *x, int64_t B, int64_t M, int64_t N, void *y,
                                 pta_stream_t stream) {
     clear_error();

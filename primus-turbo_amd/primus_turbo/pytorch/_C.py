@@ -44,6 +44,7 @@ SIGNATURES = {
     "pta_dequantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp]),
     "pta_dequantize_fp8_blockwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),
     "pta_dequantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _vp, _i32, _vp]),
+    "pta_shuffle_e8m0_scale": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "pta_grouped_dequantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "pta_transpose_u8": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "pta_grouped_compute_offs": (_i32, [_vp, _vp, _i64, _vp]),

@@ -268,9 +268,36 @@ def quant_fp8_blockwise_segment_m_row_col_impl(
 def _check_recipe(r: Optional[ScalingRecipe]):
     if r is None:
         return ScalingRecipe()
-    if r.use_sr or r.use_rht or r.shuffle_scale or r.shuffle_out:
-        raise NotImplementedError("MXFP8 shuffle / stochastic-rounding / RHT layouts are not implemented")
+    if r.use_sr or r.use_rht:
+        raise NotImplementedError("stochastic rounding and the Hadamard transform are MXFP4 features")
+    if r.shuffle_out:
+        # the reference leaves the MXFP8 output shuffle undefined (a TODO in
+        # tests/pytorch/ops/test_quantization.py:507); only the scale shuffle exists
+        raise NotImplementedError("shuffle_out is not defined for MXFP8")
     return r
+
+
+def shuffle_scale_impl(scale: torch.Tensor, layout=(16, 16)) -> torch.Tensor:
+    """E8M0 scales [M, N] -> the 16 x 16 MFMA layout [roundup(M, 256),
+    roundup(N, 8)], zero padded (shuffle_scale in csrc/pytorch/shuffle/shuffle.cpp,
+    kernel csrc/kernels/shuffle/shuffle.cu:12-73)."""
+    assert tuple(layout) == (16, 16), "Unsupported shuffle layout."
+    assert scale.dim() == 2, "Scale must be 2D"
+    assert scale.dtype in (torch.float8_e8m0fnu, torch.uint8), "Scale must be Float8_e8m0fnu."
+    x = scale.contiguous().view(torch.uint8)
+    M, N = x.shape
+    y = torch.empty((ceil_div(M, 256) * 256, ceil_div(N, 8) * 8), dtype=torch.uint8, device=x.device)
+    _C.call("pta_shuffle_e8m0_scale", _C.ptr(x), M, N, _C.ptr(y), _C.stream(x.device))
+    return y.view(torch.float8_e8m0fnu)
+
+
+def _shuffle_batched(e: torch.Tensor, G: int, rows: int) -> torch.Tensor:
+    """Scale shuffle of each of the G row blocks of e[G*rows, cols] (3-D
+    inputs keep one padded block per batch, quantization.cpp:934-955)."""
+    if G == 1:
+        return shuffle_scale_impl(e)
+    parts = [shuffle_scale_impl(e[g * rows:(g + 1) * rows]) for g in range(G)]
+    return torch.cat([p.view(torch.uint8) for p in parts]).view(torch.float8_e8m0fnu)
 
 
 def quantize_mxfp8_impl(
@@ -333,7 +360,14 @@ def quantize_mxfp8_impl(
     def shape3(t, rows):
         if exp_kmajor and t.dtype == torch.uint8:
             return t  # K-block-major exponent storage, returned as is
-        return t.view(G, rows, -1) if x.dim() == 3 else t
+        return t.view(G, -1, t.shape[-1]) if x.dim() == 3 else t
+
+    if rr.shuffle_scale or rc.shuffle_scale:
+        assert not exp_kmajor, "the scale shuffle and the K-block-major exponents are exclusive"
+        if row and rr.shuffle_scale:
+            e_row = _shuffle_batched(e_row, G, M).view(torch.uint8)
+        if col and rc.shuffle_scale:
+            e_col = _shuffle_batched(e_col, G, N).view(torch.uint8)
 
     outs = []
     if row:
@@ -371,6 +405,8 @@ def grouped_quantize_mxfp8_impl(
     rc = _check_recipe(scaling_recipe_for_trans) if with_trans else rr
     if rr.use_2d_block or rc.use_2d_block:
         raise NotImplementedError("2-D exponent blocks are not implemented for grouped MXFP8 quantization")
+    if rr.shuffle_scale or rc.shuffle_scale:
+        raise NotImplementedError("the scale shuffle is not implemented for grouped MXFP8 quantization")
     M, N = x.shape
     assert N % MXFP8_BLOCK_SIZE == 0, f"N must be divisible by {MXFP8_BLOCK_SIZE}"
     G = group_lens.numel()

@@ -65,6 +65,10 @@ def ref_lib():
         L.ref_quant_rowwise_col.argtypes = [vp, i64, i64, i64, i32, vp, vp, vp, vp, vp]
         L.ref_quant_weight.argtypes = [vp, i64, i64, i64, i32, vp, vp, vp]
         L.ref_quant_segment.argtypes = [vp, i64, i64, i64, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp]
+        if hasattr(L, "ref_shuffle_e8m0"):
+            L.ref_shuffle_e8m0.argtypes = [vp, i64, i64, vp, vp]
+        else:  # an older build of oracle/_ref without the shuffle kernel
+            L.ref_shuffle_e8m0 = None
         _ref = L
     return _ref
 

@@ -288,6 +288,44 @@ def test_mxfp8_vs_oracle(shape, qdt, use_2d):
             assert_bytes_equal(back, u8(e_ref), f"k-major {what} exponents")
 
 
+@pytest.mark.parametrize("B", [1, 4])
+@pytest.mark.parametrize("M,N", [(32, 32), (64, 256), (256, 1024), (1024, 64), (176, 160)])
+@pytest.mark.parametrize("use_2d", [False, True])
+def test_mxfp8_scale_shuffle(B, M, N, use_2d):
+    """shuffle_scale recipes give the 16 x 16 shuffle of the plain exponents
+    (the reference's test_quantize_mxfp8_shuffle); the shuffle matches the
+    oracle and, where it builds, the reference's own shuffle kernel."""
+    turbo, SG, SR = _turbo()
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import quantize_mxfp8_impl, shuffle_scale_impl
+
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn((B, M, N), generator=g).to(torch.bfloat16).cuda()
+    x2 = x.view(-1, N)
+    r = SR(use_2d_block=use_2d)
+    rs = SR(use_2d_block=use_2d, shuffle_scale=True)
+    _, er, _, ec = turbo.ops.quantize_fp8_with_trans(x2, torch.float8_e4m3fn, SG.MX_BLOCKWISE, block_size=32,
+                                                    scaling_recipe=r, scaling_recipe_for_trans=r)
+    _, ers, _, ecs = turbo.ops.quantize_fp8_with_trans(x2, torch.float8_e4m3fn, SG.MX_BLOCKWISE, block_size=32,
+                                                      scaling_recipe=rs, scaling_recipe_for_trans=rs)
+    L = ref_lib()
+    for plain, shuffled, what in ((er, ers, "row"), (ec, ecs, "col")):
+        mine = shuffle_scale_impl(plain, [16, 16])
+        assert_bytes_equal(u8(shuffled), u8(mine), f"quantize shuffle_scale {what}")
+        assert_bytes_equal(u8(mine), O.shuffle_e8m0(u8(plain)), f"shuffle vs oracle {what}")
+        if L is not None and L.ref_shuffle_e8m0 is not None:
+            ref = torch.empty_like(mine).view(torch.uint8)
+            pl = plain.contiguous().view(torch.uint8)
+            assert L.ref_shuffle_e8m0(pl.data_ptr(), pl.shape[0], pl.shape[1], ref.data_ptr(), stream()) == 0
+            torch.cuda.synchronize()
+            assert_bytes_equal(u8(mine), u8(ref), f"shuffle vs reference kernel {what}")
+    # 3-D input: one padded block per batch
+    q3, e3 = quantize_mxfp8_impl(x, torch.float8_e4m3fn, 2, 32, scaling_recipe=rs)
+    _, e3p = quantize_mxfp8_impl(x, torch.float8_e4m3fn, 2, 32, scaling_recipe=r)
+    assert e3.shape[0] == B
+    for b in range(B):
+        assert_bytes_equal(u8(e3[b]), O.shuffle_e8m0(u8(e3p[b])), f"batched shuffle {b}")
+
+
 # ---------------------------------------------------------------------------
 # dequantization
 # ---------------------------------------------------------------------------

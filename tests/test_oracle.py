@@ -271,3 +271,22 @@ def test_grouped_mx_layout_and_locality():
     _, _, _, qc2, ec2, _ = O.quant_mx_grouped(y, 0, lens)
     assert np.array_equal(qc2[:, :256], qc[:, :256]) and np.array_equal(ec2[:, :8], ec[:, :8])
     assert not np.array_equal(ec2[:, 8:16], ec[:, 8:16])
+
+
+def test_shuffle_e8m0_layout():
+    """The scale shuffle moves byte (16 h + r, 4 q + c) of each 32 x 8 tile to
+    offset 64 c + 4 r + 2 q + h, tiles in row-major order, padding to
+    [roundup(M, 256), roundup(N, 8)] with zeros (shuffle.cu:12-73)."""
+    rng = np.random.default_rng(5)
+    e = rng.integers(1, 255, size=(70, 13), dtype=np.uint8)
+    y = O.shuffle_e8m0(e)
+    assert y.shape == (256, 16)
+    flat = y.reshape(-1)
+    tiles_per_row = 16 // 8
+    for row in range(256):
+        for col in range(16):
+            tile = (row // 32) * tiles_per_row + col // 8
+            h, r = divmod(row % 32, 16)
+            q, c = divmod(col % 8, 4)
+            exp = e[row, col] if row < 70 and col < 13 else 0
+            assert flat[tile * 256 + 64 * c + 4 * r + 2 * q + h] == exp
