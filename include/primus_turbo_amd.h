@@ -333,6 +333,71 @@ int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt, const voi
                                        int64_t OUT_M, int64_t OUT_N, void *out, int c_dtype,
                                        int trans_c, int granularity, pta_stream_t stream);
 
+/* ============================================================================
+ * MoE token permutation (expert-major packing for grouped_gemm_fp8)
+ * ========================================================================== */
+
+/* expert_map kinds: bool routing map [T, E], or top-k expert indices [T, topk] */
+#define PTA_MOE_MAP_BOOL 0
+#define PTA_MOE_MAP_I32 1
+#define PTA_MOE_MAP_I64 2
+
+/* Workspace bytes needed by pta_moe_permute_preprocess. */
+size_t pta_moe_permute_preprocess_workspace_size(int64_t num_tokens, int num_local_experts);
+
+/* Slot assignment.  Each (token t, local expert e) pair routed by expert_map
+ * gets the 1-based row slot = 1 + (tokens before t routed to e) + (sum over
+ * e' < e of the counts of e' rounded up to pad_multiple).  row_id_map
+ * [num_tokens + pad_multiple, 2E + 1] int32: row t holds its slots in
+ * ascending e at [0, n), the aux value (e, or with probs_topk_stride > 0 the
+ * first k with expert_map[t, k] == e) at [E, E + n) and n at [2E]; padding row
+ * num_tokens + i holds the negated slot of the i-th padding row of each expert
+ * that has one.  Entries past n are left unwritten.  Slots above
+ * num_permuted_tokens (when > 0) are dropped and set *overflow_flag = 1.
+ * tokens_per_expert[E] int64 = padded counts (clipped by the cap);
+ * *num_dispatched = tokens routed to at least one local expert.  Index maps
+ * ignore entries outside [0, E) (after conversion to int32).  E <= 511.
+ * Replaces permute_preprocessing (csrc/pytorch/moe_permute/moe_permute.cpp:39-97,
+ * kernel csrc/kernels/moe_permute/moe_permute.cu:82-340). */
+int pta_moe_permute_preprocess(const void *expert_map, int map_kind, int64_t num_tokens,
+                               int num_local_experts, int num_topk, int pad_multiple,
+                               int64_t num_permuted_tokens, int probs_topk_stride, int32_t *row_id_map,
+                               int64_t *tokens_per_expert, int32_t *overflow_flag,
+                               int32_t *num_dispatched, void *workspace, size_t workspace_bytes,
+                               pta_stream_t stream);
+
+/* Scatter: for every row r < min(*num_dispatched + pad_multiple, row_id_map_rows)
+ * and each of its n slots d: permuted[d - 1] = tokens[r] (d > 0, r a real
+ * token) or zeros (d < 0, or r >= *num_dispatched: a padding row).  Rows are
+ * hidden * elem_bytes bytes (elem_bytes 1 for fp8, 2 for bf16/fp16; a
+ * multiple of 16).  Optional per-token fp32 scaling factors
+ * [num_tokens, scales_per_token] and probs [num_tokens, probs_stride or E]
+ * (indexed by the aux value) follow the same rows.  Slots outside
+ * [1, num_permuted] are skipped.
+ * Replaces permute (csrc/pytorch/moe_permute/moe_permute.cpp:108-204,
+ * kernel csrc/kernels/moe_permute/moe_permute.cu:437-505). */
+int pta_moe_permute(const void *tokens, int64_t num_tokens, int elem_bytes, int64_t hidden,
+                    void *permuted, int64_t num_permuted, const int32_t *row_id_map,
+                    int64_t row_id_map_rows, const int32_t *num_dispatched, int pad_multiple,
+                    int num_local_experts, const float *scaling_factor,
+                    float *permuted_scaling_factor, int scales_per_token, const float *probs,
+                    float *permuted_probs, int probs_stride, pta_stream_t stream);
+
+/* Gather-reduce: for t < min(*num_dispatched, num_tokens), tokens[t] =
+ * dtype(sum in fp32, in row_id_map order, of permuted[d - 1] over the row's
+ * positive slots d); with one expert and a probs width of 1 the single row is
+ * copied bit for bit.  dtype is PTA_BF16 or PTA_F16, hidden % 8 == 0.
+ * probs[t, :] (width probs_stride or E) = permuted_probs[d - 1] at the aux
+ * column of each positive slot, 0 elsewhere.  Rows t >= *num_dispatched are
+ * not written.
+ * Replaces unpermute (csrc/pytorch/moe_permute/moe_permute.cpp:214-276,
+ * kernels csrc/kernels/moe_permute/moe_permute.cu:507-602). */
+int pta_moe_unpermute(const void *permuted, int64_t num_permuted, int dtype, int64_t hidden,
+                      void *tokens, int64_t num_tokens, const int32_t *row_id_map,
+                      const int32_t *num_dispatched, int num_local_experts,
+                      const float *permuted_probs, float *probs, int probs_stride,
+                      pta_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,16 +1,19 @@
-// Driver for the reference's own HIP quantization kernels -- TEST INFRASTRUCTURE ONLY.
+// Driver for the reference's own HIP quantization and MoE permutation kernels --
+// TEST INFRASTRUCTURE ONLY.
 //
 // oracle/Makefile.ref compiles this file together with the reference's kernel
 // sources, where they lie under /root/reference/csrc, into oracle/_ref/libref_quant.so.
 // The extern "C" functions below replay the host-side sequence of the
 // reference's native ops (csrc/pytorch/quantization/quantization.cpp:42-206,
-// 1382-1476) on caller-provided device buffers, so GPU parity tests can compare
-// the bytes and scales of this repository's kernels with the reference's.
+// 1382-1476; csrc/pytorch/moe_permute/moe_permute.cpp:39-276) on
+// caller-provided device buffers, so GPU parity tests can compare the bytes
+// and scales of this repository's kernels with the reference's.
 // Input is bf16; fmt 0 = e4m3fn, 1 = e5m2.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
+#include "primus_turbo/moe_permute.h"
 #include "primus_turbo/quantization.h"
 #include "primus_turbo/reduce.h"
 #include "primus_turbo/shuffle.h"
@@ -130,6 +133,58 @@ int ref_shuffle_e8m0(const void *x, int64_t M, int64_t N, void *y, void *stream)
     const int64_t Mp = (M + 255) / 256 * 256, Np = (N + 7) / 8 * 8;
     shuffle_e8m0_scale(reinterpret_cast<uint8_t *>(const_cast<void *>(x)), reinterpret_cast<uint8_t *>(y), 16, 16,
                        M, N, Mp, Np, reinterpret_cast<hipStream_t>(stream));
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// MoE permutation (csrc/pytorch/moe_permute/moe_permute.cpp:39-276), on
+// caller-allocated outputs.  kind 0 = bool routing map, 1 = int32, 2 = int64
+// top-k indices.  num_dispatched must be zeroed by the caller (the reference
+// allocates it with at::zeros, moe_permute.cpp:76).
+int ref_moe_preprocess(const void *map, int kind, int64_t T, int E, int topk, int pad, int64_t cap,
+                       int probs_topk_stride, int *row_id_map, int64_t *tpe, int *overflow, int *ndisp,
+                       void *stream) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (kind == 0)
+        permute_preprocessing_impl<bool>(reinterpret_cast<const bool *>(map), topk, ndisp, E, (int)T, pad, tpe,
+                                         row_id_map, overflow, cap, probs_topk_stride, st);
+    else if (kind == 1)
+        permute_preprocessing_impl<int>(reinterpret_cast<const int *>(map), topk, ndisp, E, (int)T, pad, tpe,
+                                        row_id_map, overflow, cap, probs_topk_stride, st);
+    else
+        permute_preprocessing_impl<int64_t>(reinterpret_cast<const int64_t *>(map), topk, ndisp, E, (int)T, pad,
+                                            tpe, row_id_map, overflow, cap, probs_topk_stride, st);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// permute (moe_permute.cpp:108-204): elem_bytes 1 (fp8, optional scaling
+// factors) or 2; rim_rows = row_id_map.size(0).
+int ref_moe_permute(const void *tokens, void *out, int elem_bytes, const float *sf, float *osf, const float *probs,
+                    float *oprobs, const int *row_id_map, const int *ndisp, int pad, int E, int H, int spt,
+                    int rim_rows, int probs_stride, void *stream) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (elem_bytes == 1)
+        permute_impl<uint8_t, float, float>(reinterpret_cast<const uint8_t *>(tokens), reinterpret_cast<uint8_t *>(out),
+                                            sf, osf, probs, oprobs, row_id_map, ndisp, pad, E, H, spt, rim_rows,
+                                            probs_stride, st);
+    else
+        permute_impl<uint16_t, float, float>(reinterpret_cast<const uint16_t *>(tokens),
+                                             reinterpret_cast<uint16_t *>(out), nullptr, nullptr, probs, oprobs,
+                                             row_id_map, ndisp, pad, E, H, spt, rim_rows, probs_stride, st);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// unpermute (moe_permute.cpp:214-276): is_bf16 1 = bfloat16, 0 = float16; T = output rows.
+int ref_moe_unpermute(const void *perm, void *out, int is_bf16, const float *pprobs, float *oprobs,
+                      const int *row_id_map, const int *ndisp, int E, int H, int T, int probs_stride, void *stream) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (is_bf16)
+        unpermute_impl<dtype::bfloat16, float>(reinterpret_cast<const dtype::bfloat16 *>(perm),
+                                               reinterpret_cast<dtype::bfloat16 *>(out), pprobs, oprobs, row_id_map,
+                                               ndisp, E, H, T, probs_stride, st);
+    else
+        unpermute_impl<dtype::float16, float>(reinterpret_cast<const dtype::float16 *>(perm),
+                                              reinterpret_cast<dtype::float16 *>(out), pprobs, oprobs, row_id_map,
+                                              ndisp, E, H, T, probs_stride, st);
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 

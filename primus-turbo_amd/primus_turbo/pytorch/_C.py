@@ -21,6 +21,8 @@ PTA_TENSORWISE, PTA_ROWWISE, PTA_BLOCKWISE, PTA_MX_BLOCKWISE = 1, 2, 3, 4
 DUAL_COL_TRANSPOSED, DUAL_ROW_SCALE_KMAJOR = 1, 2
 # exponent layout flag of pta_quantize_mxfp8
 MX_EXP_KMAJOR = 1
+# expert_map kinds of pta_moe_permute_preprocess
+MOE_MAP_BOOL, MOE_MAP_I32, MOE_MAP_I64 = 0, 1, 2
 
 _vp, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
 
@@ -78,6 +80,16 @@ SIGNATURES = {
         _i32,
         [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
     ),
+    "pta_moe_permute_preprocess_workspace_size": (_sz, [_i64, _i32]),
+    "pta_moe_permute_preprocess": (
+        _i32,
+        [_vp, _i32, _i64, _i32, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "pta_moe_permute": (
+        _i32,
+        [_vp, _i64, _i32, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _vp],
+    ),
+    "pta_moe_unpermute": (_i32, [_vp, _i64, _i32, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp]),
 }
 
 _lib = None

@@ -8,3 +8,4 @@ from primus_turbo.pytorch.ops.quantization import (  # noqa: F401
     quantize_fp8,
     quantize_fp8_with_trans,
 )
+from primus_turbo.pytorch.ops.moe import moe_permute, moe_unpermute  # noqa: F401

@@ -69,6 +69,12 @@ def ref_lib():
             L.ref_shuffle_e8m0.argtypes = [vp, i64, i64, vp, vp]
         else:  # an older build of oracle/_ref without the shuffle kernel
             L.ref_shuffle_e8m0 = None
+        if hasattr(L, "ref_moe_preprocess"):
+            L.ref_moe_preprocess.argtypes = [vp, i32, i64, i32, i32, i32, i64, i32, vp, vp, vp, vp, vp]
+            L.ref_moe_permute.argtypes = [vp, vp, i32, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
+            L.ref_moe_unpermute.argtypes = [vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, vp]
+        else:  # an older build of oracle/_ref without the MoE permutation kernels
+            L.ref_moe_preprocess = None
         _ref = L
     return _ref
 
