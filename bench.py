@@ -343,6 +343,33 @@ def _other_configs(args):
                                                          _mx_strides(ea5), False, ew5, _mx_strides(ew5), False,
                                                          out=o5), it, 2), 2.0 * 8192 * 28672 * 8192),
     }
+    del a5, w5, qa5, qw5, o5
+
+    # MoE token permutation producing config 4's operand shape: 8192 dispatched
+    # tokens, each routed to 8 of the 32 local experts, hidden 7168 -> 65536
+    # expert-major rows (and the inverse reduction)
+    from primus_turbo.pytorch.kernels.moe.moe_permute_impl import (
+        permute_impl,
+        permute_preprocessing_impl,
+        unpermute_impl,
+    )
+
+    T6, E6, k6, H6 = 8192, 32, 8, 7168
+    idx6 = torch.sort(torch.argsort(torch.rand((T6, E6), generator=g), dim=1)[:, :k6], dim=1).values.to(dev)
+    pre = lambda: permute_preprocessing_impl(idx6, E6, k6, 0, -1, 0)  # noqa: E731
+    rim6, tpe6, _, nd6 = pre()
+    P6 = int(tpe6.sum().item())
+    tok6 = torch.randn((T6, H6), generator=g).bfloat16().to(dev)
+    out6 = torch.empty((P6, H6), dtype=torch.bfloat16, device=dev)
+    back6 = torch.empty((T6, H6), dtype=torch.bfloat16, device=dev)
+    nb6 = (T6 + P6) * H6 * 2
+    res["moe_permute_8192x7168_top8_of_32"] = {
+        "preprocess": {"ms": round(_time_cuda(pre, it, 3), 4)},
+        "permute": _quant_rec(_time_cuda(lambda: permute_impl(tok6, out6, None, None, None, None, rim6, nd6, 0, E6, H6,
+                                                              0, False, False, P6, 0), it, 3), nb6),
+        "unpermute": _quant_rec(_time_cuda(lambda: unpermute_impl(out6, back6, None, None, rim6, nd6, E6, H6, False, 0),
+                                           it, 3), nb6),
+    }
     return res
 
 
