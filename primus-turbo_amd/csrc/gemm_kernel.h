@@ -207,7 +207,12 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     void          *C  = g.c;
     int64_t        kb_base = 0; // first global K block of this problem (group_mode 2)
     if (g.group_mode == 1) {
-        const int64_t id = blockIdx.x;
+        // XCD-aware order: workgroups are dispatched round-robin over the 8
+        // XCDs, so XCD x takes M-tile rows x, x + 8, ... each with all of the
+        // row's N-tiles, and a row's A tile is fetched into one XCD's L2 only
+        // (tiles_m is a multiple of 8 in this mode; surplus rows exit below).
+        const int64_t b8 = blockIdx.x >> 3;
+        const int64_t id = (8 * (b8 / g.tiles_n) + (blockIdx.x & 7)) * g.tiles_n + b8 % g.tiles_n;
         const int64_t mt = id / g.tiles_n, tn = id % g.tiles_n;
         int64_t       cum = 0, grp = -1, gstart = 0, gend = 0;
         for (int64_t q = 0; q < g.G; ++q) {

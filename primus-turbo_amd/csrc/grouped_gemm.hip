@@ -153,9 +153,10 @@ extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scal
     } else {
         g.sa_bytes = 4; g.sb_bytes = 4; g.sb_gstride = 0; // one scalar shared by all groups
     }
-    // grid upper bound: every group may add one partial tile
+    // grid upper bound: every group may add one partial tile; rows rounded up
+    // to a multiple of 8 for the kernel's XCD-aware tile order
     g.tiles_n = static_cast<int>(cdiv(N, BN));
-    g.tiles_m = static_cast<int>(cdiv(M_total, BM) + G);
+    g.tiles_m = static_cast<int>(cdiv(cdiv(M_total, BM) + G, 8) * 8);
     if (int rc = run(g, sm, false, b2d, a_fmt, b_fmt, c_dtype, st)) return rc;
     zero_tail_kernel<<<64, 256, 0, st>>>(group_offs_out ? group_offs_out : group_offs, G, M_total,
                                          N * static_cast<int64_t>(eb), static_cast<uint8_t *>(out));
