@@ -523,3 +523,145 @@ def transpose_fp8(x: torch.Tensor) -> torch.Tensor:
         y = torch.empty((B, N, M), dtype=x.dtype, device=x.device)
     _C.call("pta_transpose_u8", _C.ptr(x), B, M, N, _C.ptr(y), _C.stream(x.device))
     return y
+
+
+# ---------------------------------------------------------------------------
+# torch.compile support: the public quantize / dequantize ops are also
+# registered as opaque custom ops with shape-only fake implementations, as the
+# reference registers its impls (quantization_impl.py:74-486, native Meta
+# kernels at csrc/pytorch/bindings_pytorch.cpp:182-231).  Eager calls keep the
+# direct path: the custom-op dispatcher adds ~15 us of host time per call.
+# ---------------------------------------------------------------------------
+def _register(name: str, schema: str, impl, fake) -> None:
+    op = torch.library.custom_op(f"primus_turbo_amd::{name}", impl, mutates_args=(), schema=schema)
+    op.register_fake(fake)
+
+
+def impl_for(name: str, raw):
+    """``raw`` in eager mode; the registered custom op while torch.compile traces."""
+    if torch.compiler.is_compiling():
+        return getattr(torch.ops.primus_turbo_amd, name)
+    return raw
+
+
+def _f32(shape, like: torch.Tensor) -> torch.Tensor:
+    return torch.empty(shape, dtype=torch.float32, device=like.device)
+
+
+def _fake_rowwise(x, out_dtype, axis, scale=None):
+    ax = axis % x.dim()
+    sshape = list(x.shape)
+    sshape[ax] = 1
+    return torch.empty(x.shape, dtype=out_dtype, device=x.device), _f32(sshape, x)
+
+
+def _fake_block(x, dtype, axis, block_size=128):
+    M, N = x.shape
+    sshape = (M, ceil_div(N, block_size)) if axis % 2 == 1 else (ceil_div(M, block_size), N)
+    return torch.empty((M, N), dtype=dtype, device=x.device), _f32(sshape, x)
+
+
+def _fake_dual(x, dtype, block_size=128):
+    M, N = x.shape
+    return (torch.empty((M, N), dtype=dtype, device=x.device), _f32((M, ceil_div(N, block_size)), x),
+            torch.empty((M, N), dtype=dtype, device=x.device), _f32((ceil_div(M, block_size), N), x))
+
+
+def _fake_weight(w, dtype, block_size=128):
+    lead = tuple(w.shape[:-2])
+    M, N = w.shape[-2], w.shape[-1]
+    return (torch.empty(w.shape, dtype=dtype, device=w.device),
+            _f32(lead + (ceil_div(M, block_size), ceil_div(N, block_size)), w))
+
+
+_register("quantize_fp8_tensorwise", "(Tensor x, ScalarType out_dtype, Tensor? scale=None) -> (Tensor, Tensor)",
+          quantize_fp8_tensorwise_impl,
+          lambda x, out_dtype, scale=None: (torch.empty(x.shape, dtype=out_dtype, device=x.device), _f32((), x)))
+_register("quantize_fp8_rowwise", "(Tensor x, ScalarType out_dtype, int axis, Tensor? scale=None) -> (Tensor, Tensor)",
+          quantize_fp8_rowwise_impl, _fake_rowwise)
+_register("dequantize_fp8_tensorwise", "(Tensor x, ScalarType out_dtype, Tensor scale_inv) -> Tensor",
+          dequantize_fp8_tensorwise_impl,
+          lambda x, out_dtype, scale_inv: torch.empty(x.shape, dtype=out_dtype, device=x.device))
+_register("dequantize_fp8_rowwise", "(Tensor x, ScalarType out_dtype, int axis, Tensor scale_inv) -> Tensor",
+          dequantize_fp8_rowwise_impl,
+          lambda x, out_dtype, axis, scale_inv: torch.empty(x.shape, dtype=out_dtype, device=x.device))
+_register("quant_fp8_blockwise", "(Tensor x, ScalarType dtype, int axis, int block_size=128) -> (Tensor, Tensor)",
+          quant_fp8_blockwise_impl, _fake_block)
+_register("quant_fp8_blockwise_dual", "(Tensor x, ScalarType dtype, int block_size=128) -> (Tensor, Tensor, Tensor, Tensor)",
+          lambda x, dtype, block_size=128: quant_fp8_blockwise_dual_impl(x, dtype, block_size), _fake_dual)
+_register("quant_fp8_blockwise_for_weight", "(Tensor w, ScalarType dtype, int block_size=128) -> (Tensor, Tensor)",
+          lambda w, dtype, block_size=128: tuple(t.contiguous() for t in quant_fp8_blockwise_for_weight_impl(w, dtype, block_size)),
+          _fake_weight)
+_register("dequant_fp8_blockwise",
+          "(Tensor x_fp8, Tensor scale_inv, ScalarType out_dtype, int axis, int block_size=128) -> Tensor",
+          dequant_fp8_blockwise_impl,
+          lambda x_fp8, scale_inv, out_dtype, axis, block_size=128: torch.empty(x_fp8.shape, dtype=out_dtype,
+                                                                                device=x_fp8.device))
+_register("dequant_fp8_blockwise_for_weight",
+          "(Tensor w_fp8, Tensor scale_inv, ScalarType out_dtype, int block_size=128) -> Tensor",
+          dequant_fp8_blockwise_for_weight_impl,
+          lambda w_fp8, scale_inv, out_dtype, block_size=128: torch.empty(w_fp8.shape, dtype=out_dtype,
+                                                                          device=w_fp8.device))
+
+
+def _mx_impl_flat(x, out_dtype, axis, block_size, with_trans, use_2d_row, shuffle_row, use_2d_col, shuffle_col):
+    rr = ScalingRecipe(use_2d_block=use_2d_row, shuffle_scale=shuffle_row)
+    rc = ScalingRecipe(use_2d_block=use_2d_col, shuffle_scale=shuffle_col)
+    return list(quantize_mxfp8_impl(x, out_dtype, axis, block_size, with_trans, rr, rc if with_trans else None))
+
+
+def _mx_fake_flat(x, out_dtype, axis, block_size, with_trans, use_2d_row, shuffle_row, use_2d_col, shuffle_col):
+    G, M, N = (1, x.shape[0], x.shape[1]) if x.dim() == 2 else tuple(x.shape)
+    Mp, Np = ceil_div(M, MXFP8_PADDING_ALIGN_SIZE) * 128, ceil_div(N, MXFP8_PADDING_ALIGN_SIZE) * 128
+    if with_trans:
+        row, col = True, True
+    else:
+        row = axis == (1 if x.dim() == 2 else 2)
+        col = not row
+    e8 = torch.float8_e8m0fnu
+
+    def pair(rows, cols, shuffle):
+        q = torch.empty((G * rows, cols), dtype=out_dtype, device=x.device)
+        if shuffle:
+            e = torch.empty((G * ceil_div(rows, 256) * 256, ceil_div(cols // 32, 8) * 8), dtype=e8, device=x.device)
+        else:
+            e = torch.empty((G * rows, cols // 32), dtype=e8, device=x.device)
+        if x.dim() == 3:
+            q, e = q.view(G, -1, q.shape[-1]), e.view(G, -1, e.shape[-1])
+        return [q, e]
+
+    outs = []
+    if row:
+        outs += pair(M, Np, shuffle_row)
+    if col:
+        outs += pair(N, Mp, shuffle_col)
+    return outs
+
+
+def _mx_deq_fake(x, out_dtype, axis, block_size, scale_inv):
+    rowwise = axis == (1 if x.dim() == 2 else 2)
+    shape = list(x.shape)
+    if not rowwise:
+        shape[-1], shape[-2] = shape[-2], shape[-1]
+    return torch.empty(shape, dtype=out_dtype, device=x.device)
+
+
+_register("quantize_mxfp8",
+          "(Tensor x, ScalarType out_dtype, int? axis, int block_size, bool with_trans, bool use_2d_row, "
+          "bool shuffle_row, bool use_2d_col, bool shuffle_col) -> Tensor[]", _mx_impl_flat, _mx_fake_flat)
+_register("dequantize_mxfp8", "(Tensor x, ScalarType out_dtype, int axis, int block_size, Tensor scale_inv) -> Tensor",
+          dequantize_mxfp8_impl, _mx_deq_fake)
+
+
+def quantize_mxfp8_op(x, out_dtype, axis, block_size, with_trans=False, scaling_recipe=None,
+                      scaling_recipe_for_trans=None):
+    """quantize_mxfp8_impl for the public ops: the direct call in eager mode,
+    the registered custom op (recipes passed as flags) under torch.compile."""
+    if not torch.compiler.is_compiling():
+        return quantize_mxfp8_impl(x, out_dtype, axis, block_size, with_trans, scaling_recipe,
+                                   scaling_recipe_for_trans)
+    rr = _check_recipe(scaling_recipe)
+    rc = _check_recipe(scaling_recipe_for_trans) if with_trans else rr
+    return tuple(torch.ops.primus_turbo_amd.quantize_mxfp8(x, out_dtype, axis, block_size, with_trans,
+                                                           rr.use_2d_block, rr.shuffle_scale, rc.use_2d_block,
+                                                           rc.shuffle_scale))

@@ -20,12 +20,13 @@ from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
     dequantize_mxfp8_impl,
     grouped_dequantize_mxfp8_impl,
     grouped_quantize_mxfp8_impl,
+    impl_for,
+    quantize_mxfp8_op,
     quant_fp8_blockwise_dual_impl,
     quant_fp8_blockwise_for_weight_impl,
     quant_fp8_blockwise_impl,
     quantize_fp8_rowwise_impl,
     quantize_fp8_tensorwise_impl,
-    quantize_mxfp8_impl,
 )
 
 __all__ = [
@@ -56,18 +57,18 @@ def quantize_fp8(
     axis 1 (2D) / 2 (3D) is rowwise, axis 0 / 1 is colwise with transposed output.
     """
     if granularity == ScalingGranularity.TENSORWISE:
-        return quantize_fp8_tensorwise_impl(x, out_dtype)
+        return impl_for("quantize_fp8_tensorwise", quantize_fp8_tensorwise_impl)(x, out_dtype)
     elif granularity == ScalingGranularity.ROWWISE:
-        return quantize_fp8_rowwise_impl(x, out_dtype, axis)
+        return impl_for("quantize_fp8_rowwise", quantize_fp8_rowwise_impl)(x, out_dtype, axis)
     elif granularity == ScalingGranularity.BLOCKWISE:
         assert block_size is not None, "block_size must be specified for BLOCKWISE quantization"
         if scaling_recipe is not None and scaling_recipe.use_2d_block:
-            return quant_fp8_blockwise_for_weight_impl(x, out_dtype, block_size=block_size)
+            return impl_for("quant_fp8_blockwise_for_weight", quant_fp8_blockwise_for_weight_impl)(x, out_dtype, block_size)
         assert axis is not None, "axis must be specified for 1D BLOCKWISE quantization"
-        return quant_fp8_blockwise_impl(x, out_dtype, axis=axis, block_size=block_size)
+        return impl_for("quant_fp8_blockwise", quant_fp8_blockwise_impl)(x, out_dtype, axis, block_size)
     elif granularity == ScalingGranularity.MX_BLOCKWISE:
         assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
-        return quantize_mxfp8_impl(x, out_dtype, axis, block_size, False, scaling_recipe)
+        return quantize_mxfp8_op(x, out_dtype, axis, block_size, False, scaling_recipe)
     else:
         raise NotImplementedError(f"Unknown granularity {granularity}")
 
@@ -84,9 +85,9 @@ def quantize_fp8_with_trans(
     """Row- and column-direction quantization in one pass: (q_row, s_row, q_col, s_col)."""
     if granularity == ScalingGranularity.MX_BLOCKWISE:
         assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
-        return quantize_mxfp8_impl(x, out_dtype, None, block_size, True, scaling_recipe, scaling_recipe_for_trans)
+        return quantize_mxfp8_op(x, out_dtype, None, block_size, True, scaling_recipe, scaling_recipe_for_trans)
     elif granularity == ScalingGranularity.BLOCKWISE:
-        return quant_fp8_blockwise_dual_impl(x, out_dtype, block_size=block_size)
+        return impl_for("quant_fp8_blockwise_dual", quant_fp8_blockwise_dual_impl)(x, out_dtype, block_size)
     else:
         raise NotImplementedError(f"Unknown granularity {granularity}")
 
@@ -144,20 +145,21 @@ def dequantize_fp8(
 ):
     """FP8 dequantize: out_dtype(float(x) * scale_inv) with the granularity's scale layout."""
     if granularity == ScalingGranularity.TENSORWISE:
-        return dequantize_fp8_tensorwise_impl(x, out_dtype, scale_inv)
+        return impl_for("dequantize_fp8_tensorwise", dequantize_fp8_tensorwise_impl)(x, out_dtype, scale_inv)
     elif granularity == ScalingGranularity.ROWWISE:
         if axis is None:
             raise ValueError("axis must be specified for rowwise FP8 de-quantization")
-        return dequantize_fp8_rowwise_impl(x, out_dtype, axis, scale_inv)
+        return impl_for("dequantize_fp8_rowwise", dequantize_fp8_rowwise_impl)(x, out_dtype, axis, scale_inv)
     elif granularity == ScalingGranularity.BLOCKWISE:
         assert block_size is not None, "block_size must be specified for BLOCKWISE de-quantization"
         if scaling_recipe is not None and scaling_recipe.use_2d_block:
-            return dequant_fp8_blockwise_for_weight_impl(x, scale_inv, out_dtype, block_size)
+            return impl_for("dequant_fp8_blockwise_for_weight", dequant_fp8_blockwise_for_weight_impl)(
+                x, scale_inv, out_dtype, block_size)
         assert axis is not None, "axis must be specified for 1D BLOCKWISE de-quantization"
-        return dequant_fp8_blockwise_impl(x, scale_inv, out_dtype, axis, block_size)
+        return impl_for("dequant_fp8_blockwise", dequant_fp8_blockwise_impl)(x, scale_inv, out_dtype, axis, block_size)
     elif granularity == ScalingGranularity.MX_BLOCKWISE:
         assert block_size == MXFP8_BLOCK_SIZE, f"The block size must be {MXFP8_BLOCK_SIZE} for MXFP8 quantization"
-        return dequantize_mxfp8_impl(x, out_dtype, axis, block_size, scale_inv)
+        return impl_for("dequantize_mxfp8", dequantize_mxfp8_impl)(x, out_dtype, axis, block_size, scale_inv)
     else:
         raise NotImplementedError(f"Unknown granularity {granularity}")
 
