@@ -86,6 +86,7 @@ struct GemmArgs {
                                    // same rows as A)
     int64_t        G;
     int64_t        b_gstride, sb_gstride, c_gstride; // elements / bytes per group
+    int            persistent; // > 0: a grid of that many workgroups loops over the tiles_m * tiles_n tiles
 };
 
 // gfx950 serves a ds_read_b128 two 8-lane groups per clock; with the chunk
@@ -184,8 +185,47 @@ __device__ __forceinline__ void wait_dma_and_barrier() {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT>
-__global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Group of M-tile row `mt` in grouped mode 1: the wave computes every group's
+// tile count (ceil(rows / BM)) and their prefix sums 64 groups at a time and
+// picks the group whose tile range holds `mt` with one ballot.  Returns -1
+// past the last tile.
+__device__ __forceinline__ int64_t find_tile_group(const int64_t *offs, int64_t G, int64_t mt,
+                                                   int64_t &first_tile, int64_t &gstart, int64_t &gend) {
+    const int lane = threadIdx.x & 63;
+    int64_t   base = 0;
+    for (int64_t q0 = 0; q0 < G; q0 += 64) {
+        const int64_t q  = q0 + lane;
+        const int64_t s0 = q < G ? offs[q] : 0, s1 = q < G ? offs[q + 1] : 0;
+        const int64_t nt = q < G ? (s1 - s0 + BM - 1) / BM : 0;
+        int64_t       incl = nt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int64_t o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        const int64_t  start = base + incl - nt;
+        const uint64_t hit   = __ballot(nt > 0 && mt >= start && mt < start + nt);
+        if (hit != 0) {
+            // wave-uniform results (scalar registers for the tile's address arithmetic)
+            const int src = __builtin_ctzll(hit);
+            first_tile    = uniform64(__shfl(start, src, 64));
+            gstart        = uniform64(__shfl(s0, src, 64));
+            gend          = uniform64(__shfl(s1, src, 64));
+            return q0 + src;
+        }
+        base += uniform64(__shfl(incl, 63, 64));
+    }
+    return -1;
+}
+
+template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT, bool PERSIST>
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) {
     using CF = TileCfg<BNT>;
     constexpr int BN_ = CF::BN_, WTN_ = CF::WTN_, TN_ = CF::TN_, TILE_B_ = CF::TILE_B_, STAGE_ = CF::STAGE_;
     constexpr int SSLOT_ = CF::SSLOT_, SBASE_ = CF::SBASE_, EPITCH_ = CF::EPITCH_;
@@ -193,7 +233,10 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     // LDS byte address of the dynamic shared buffer (M0 operand of the DMA)
     const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)(__attribute__((address_space(3))) uint8_t *)(smem));
 
-    const int t    = threadIdx.x;
+    // persistent loop: an opaque copy of the lane id makes the lane-derived
+    // addressing be recomputed per tile instead of held (or spilled) across tiles
+    int t = threadIdx.x;
+    if constexpr (PERSIST) asm volatile("" : "+v"(t));
     const int lane = t & 63;
     const int wave = t >> 6;
     const int wm   = wave / WGN;
@@ -211,17 +254,12 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
         // XCDs, so XCD x takes M-tile rows x, x + 8, ... each with all of the
         // row's N-tiles, and a row's A tile is fetched into one XCD's L2 only
         // (tiles_m is a multiple of 8 in this mode; surplus rows exit below).
-        const int64_t b8 = blockIdx.x >> 3;
-        const int64_t id = (8 * (b8 / g.tiles_n) + (blockIdx.x & 7)) * g.tiles_n + b8 % g.tiles_n;
+        const int64_t b8 = bid >> 3;
+        const int64_t id = (8 * (b8 / g.tiles_n) + (bid & 7)) * g.tiles_n + b8 % g.tiles_n;
         const int64_t mt = id / g.tiles_n, tn = id % g.tiles_n;
-        int64_t       cum = 0, grp = -1, gstart = 0, gend = 0;
-        for (int64_t q = 0; q < g.G; ++q) {
-            const int64_t s0 = g.group_offs[q], s1 = g.group_offs[q + 1];
-            const int64_t nt = (s1 - s0 + BM - 1) / BM;
-            if (mt < cum + nt) { grp = q; gstart = s0; gend = s1; break; }
-            cum += nt;
-        }
-        if (grp < 0) return; // past the last tile (grid is an upper bound)
+        int64_t       cum = 0, gstart = 0, gend = 0;
+        const int64_t grp = find_tile_group(g.group_offs, g.G, mt, cum, gstart, gend);
+        if (grp < 0) return; // past the last tile (the tile count is an upper bound)
         m0 = gstart + (mt - cum) * BM;
         M  = gend; // rows [m0, gend) are valid
         if (g.group_offs_out != nullptr) {
@@ -237,7 +275,7 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
         B  = g.b + grp * g.b_gstride;
         SB = reinterpret_cast<const uint8_t *>(g.sb) + grp * g.sb_gstride;
     } else {
-        int       id    = blockIdx.x;
+        int       id    = static_cast<int>(bid);
         const int total = g.tiles_m * g.tiles_n;
         if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
         const int per_group = g.group_m * g.tiles_n;
@@ -560,9 +598,27 @@ __global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
     }
 }
 
-template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT>
-int launch_one(const GemmArgs &g, hipStream_t st) {
-    auto kern = gemm_nt_kernel<SM, A2D, B2D, FA, FB, OUT_DT, BNT>;
+// PERSIST (grouped mode 1): a grid of at most one workgroup per CU walks the
+// tile list, workgroup b taking tiles b, b + gridDim.x, ...; the barrier keeps
+// the next tile's operand DMAs out of LDS until every wave has finished reading
+// the previous tile's epilogue staging.  The dense kernels stay loop-free (a
+// loop around the tile body costs them registers and ~5% in time).
+template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT, bool PERSIST>
+__global__ __launch_bounds__(NTHR) void gemm_nt_kernel(const GemmArgs g) {
+    if constexpr (PERSIST) {
+        const int total = g.tiles_m * g.tiles_n;
+        for (int it = static_cast<int>(blockIdx.x); it < total; it += static_cast<int>(gridDim.x)) {
+            if (it != static_cast<int>(blockIdx.x)) __syncthreads();
+            gemm_tile<SM, A2D, B2D, FA, FB, OUT_DT, BNT, true>(g, it);
+        }
+    } else {
+        gemm_tile<SM, A2D, B2D, FA, FB, OUT_DT, BNT, false>(g, blockIdx.x);
+    }
+}
+
+template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT, bool PERSIST>
+int launch_kernel(const GemmArgs &g, hipStream_t st) {
+    auto kern = gemm_nt_kernel<SM, A2D, B2D, FA, FB, OUT_DT, BNT, PERSIST>;
     constexpr size_t smem = TileCfg<BNT>::SMEM;
     static bool configured = false; // idempotent attribute set, benign race
     if (!configured) {
@@ -570,11 +626,19 @@ int launch_one(const GemmArgs &g, hipStream_t st) {
                                           hipFuncAttributeMaxDynamicSharedMemorySize, smem));
         configured = true;
     }
-    const dim3 grid(static_cast<uint32_t>(g.tiles_m * g.tiles_n),
-                    static_cast<uint32_t>(g.group_mode == 2 ? g.G : 1));
+    const uint32_t ntiles = static_cast<uint32_t>(g.tiles_m * g.tiles_n);
+    const uint32_t np     = static_cast<uint32_t>(g.persistent);
+    const dim3     grid(g.persistent > 0 ? (np < ntiles ? np : ntiles) : ntiles,
+                        static_cast<uint32_t>(g.group_mode == 2 ? g.G : 1));
     kern<<<grid, NTHR, smem, st>>>(g);
     PTA_CHECK_LAUNCH();
     return PTA_OK;
+}
+
+template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT>
+int launch_one(const GemmArgs &g, hipStream_t st) {
+    if (g.persistent > 0) return launch_kernel<SM, A2D, B2D, FA, FB, OUT_DT, BNT, true>(g, st);
+    return launch_kernel<SM, A2D, B2D, FA, FB, OUT_DT, BNT, false>(g, st);
 }
 
 // Only the 256-wide tile is instantiated: a measured split of the last round

@@ -85,6 +85,19 @@ int gran_sm(int gran) {
     }
 }
 
+// Compute units of the current device (cached per device id).
+int cu_count() {
+    static int cached[64] = {0};
+    int        dev        = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n; // benign race: every writer stores the same value
+    }
+    return cached[dev];
+}
+
 int run(GemmArgs &g, int sm, bool a2d, bool b2d, int fa, int fb, int out_dt, hipStream_t st) {
     if (sm == SM_TENSOR) return dispatch_tensor(g, fa, fb, out_dt, st);
     if (sm == SM_ROW) return dispatch_row(g, fa, fb, out_dt, st);
@@ -109,9 +122,9 @@ extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scal
                                     int granularity, int num_cu, void *workspace, size_t workspace_bytes,
                                     pta_stream_t stream) {
     clear_error();
-    (void)num_cu;
     const int sm = gran_sm(granularity);
     PTA_CHECK_ARG(sm >= 0, "unknown granularity %d", granularity);
+    PTA_CHECK_ARG(num_cu >= 0, "num_cu must be >= 0 (0: all compute units)");
     PTA_CHECK_ARG(a && b && out && a_scale && b_scale && group_offs, "NULL pointer argument");
     PTA_CHECK_ARG(G >= 1 && M_total >= 0 && N >= 0 && K >= 0, "bad shape");
     PTA_CHECK_ARG(K % 16 == 0, "K must be a multiple of 16");
@@ -153,10 +166,14 @@ extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scal
     } else {
         g.sa_bytes = 4; g.sb_bytes = 4; g.sb_gstride = 0; // one scalar shared by all groups
     }
-    // grid upper bound: every group may add one partial tile; rows rounded up
-    // to a multiple of 8 for the kernel's XCD-aware tile order
-    g.tiles_n = static_cast<int>(cdiv(N, BN));
-    g.tiles_m = static_cast<int>(cdiv(cdiv(M_total, BM) + G, 8) * 8);
+    // tile-list upper bound: every group may add one partial tile; rows rounded
+    // up to a multiple of 8 for the kernel's XCD-aware tile order.  Persistent
+    // grid: one workgroup per CU (the tile uses most of a CU's LDS), or
+    // num_cu of them, which leaves the other CUs free for concurrent work.
+    g.tiles_n    = static_cast<int>(cdiv(N, BN));
+    g.tiles_m    = static_cast<int>(cdiv(cdiv(M_total, BM) + G, 8) * 8);
+    const int cu = cu_count();
+    g.persistent = num_cu > 0 && num_cu < cu ? num_cu : cu;
     if (int rc = run(g, sm, false, b2d, a_fmt, b_fmt, c_dtype, st)) return rc;
     zero_tail_kernel<<<64, 256, 0, st>>>(group_offs_out ? group_offs_out : group_offs, G, M_total,
                                          N * static_cast<int64_t>(eb), static_cast<uint8_t *>(out));

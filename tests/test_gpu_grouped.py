@@ -233,3 +233,28 @@ def test_grouped_mx_gemm_fwd_and_wgrad_vs_oracle(lens):
             assert not w_out[g].any()
             continue
         _check(w_out[g], O.gemm_ref(dgc[:, c0:c1], dac[:, c0:c1], False, True), f"wgrad group {g}")
+
+
+@pytest.mark.parametrize("gran", ["BLOCKWISE", "TENSORWISE", "MX_BLOCKWISE"])
+def test_grouped_gemm_num_cu(gran):
+    """num_cu (grouped_gemm_fp8.py:808-904) sizes the persistent grid: any
+    value gives the same bits as all CUs (each tile is computed the same way
+    whichever workgroup takes it); tiles past the grid wrap to the next pass."""
+    (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
+    g = getattr(SG, gran)
+    if gran == "MX_BLOCKWISE":
+        from primus_turbo.pytorch.core.low_precision import ScaleDtype
+
+        cfg = Cfg(granularity=g, format=Format.E4M3, block_size=32, scale_dtype=ScaleDtype.E8M0)
+    else:
+        cfg = Cfg(granularity=g, format=Format.E4M3, block_size=128 if gran == "BLOCKWISE" else None)
+    lens = [700, 0, 1300, 256, 1]
+    G, K, N = len(lens), 512, 768
+    gen = torch.Generator().manual_seed(4)
+    a = torch.randn((sum(lens), K), generator=gen).bfloat16().cuda()
+    w = torch.randn((G, N, K), generator=gen).bfloat16().cuda()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    ref = turbo.ops.grouped_gemm_fp8(a, w, gl, trans_b=True, config=cfg)
+    for ncu in (1, 7, 8, 37, 100000):
+        out = turbo.ops.grouped_gemm_fp8(a, w, gl, trans_b=True, config=cfg, num_cu=ncu)
+        assert torch.equal(out, ref), f"num_cu={ncu}"
