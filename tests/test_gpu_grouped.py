@@ -258,3 +258,32 @@ def test_grouped_gemm_num_cu(gran):
     for ncu in (1, 7, 8, 37, 100000):
         out = turbo.ops.grouped_gemm_fp8(a, w, gl, trans_b=True, config=cfg, num_cu=ncu)
         assert torch.equal(out, ref), f"num_cu={ncu}"
+
+
+def test_grouped_gemm_many_groups():
+    """300 groups, most of them empty or a few rows: the persistent scheduler's
+    group lookup walks several 64-group chunks.  Every group holds the
+    reference's grouped criterion against its fp32 product (> 25 dB for e4m3,
+    tests/pytorch/ops/test_grouped_gemm_fp8.py:163-175), and a 3-CU grid gives
+    the same bits."""
+    (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
+    gen = torch.Generator().manual_seed(21)
+    G, K, N = 300, 256, 256
+    lens = torch.randint(0, 12, (G,), generator=gen)
+    lens[torch.randperm(G, generator=gen)[:200]] = 0
+    lens[7] = 300
+    lens_l = [int(v) for v in lens]
+    a = torch.randn((sum(lens_l), K), generator=gen).bfloat16().cuda()
+    w = (torch.randn((G, N, K), generator=gen) * 0.05).bfloat16().cuda()
+    gl = lens.cuda()
+    cfg = Cfg(granularity=SG.TENSORWISE, format=Format.E4M3)
+    out = turbo.ops.grouped_gemm_fp8(a, w, gl, trans_b=True, config=cfg)
+    ref = turbo.ops.grouped_gemm_fp8(a, w, gl, trans_b=True, config=cfg, num_cu=3)
+    assert torch.equal(out, ref)
+    off = 0
+    for g_, L in enumerate(lens_l):
+        if L:
+            ref_g = a[off:off + L].float() @ w[g_].float().T
+            s = O.snr_db(f32(ref_g), f32(out[off:off + L]))
+            assert s > 25, f"group {g_}: SNR {s:.1f} dB vs the fp32 product"
+        off += L
