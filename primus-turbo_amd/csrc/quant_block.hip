@@ -68,15 +68,18 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     if constexpr ((MODE & QB_SEGMENT) != 0) {
         const int64_t M_padded = args.padded_offs[args.G];
         if (pad_row0 >= M_padded) return;
-        // binary search over the non-decreasing padded offsets
-        int64_t lo = 0, hi = args.G - 1;
-        while (lo < hi) {
-            const int64_t mid = (lo + hi + 1) >> 1;
-            if (args.padded_offs[mid] <= pad_row0) lo = mid;
-            else hi = mid - 1;
+        // the last g with padded_offs[g] <= pad_row0 owns a non-empty segment.
+        // The offsets are non-decreasing, so the lanes' comparisons over 64
+        // consecutive groups form a prefix and one ballot counts it: one round
+        // of loads per 64 groups instead of a chain of dependent ones.
+        int64_t g = 0;
+        for (int64_t q0 = 0; q0 < args.G; q0 += 64) {
+            const int64_t  q    = q0 + lane;
+            const bool     le   = q < args.G && args.padded_offs[q] <= pad_row0;
+            const int      cnt  = __popcll(__ballot(le));
+            if (cnt > 0) g = q0 + cnt - 1;
+            if (cnt < 64) break;
         }
-        // the last g with padded_offs[g] <= pad_row0 owns a non-empty segment
-        const int64_t g = lo;
         const int64_t orig_start = args.group_offs[g];
         const int64_t orig_end   = args.group_offs[g + 1];
         const int64_t pad_start  = args.padded_offs[g];
