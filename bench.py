@@ -346,7 +346,25 @@ def _other_configs(args):
                                                                               SG.BLOCKWISE.value), it),
                                       2.0 * 65536 * 2048 * 7168),
     }
-    del a4, w4, ar4, wq4
+    del ar4, wq4
+    # the whole grouped layer step through the public op: quantize + fwd + dgrad + variable-K wgrad
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import Float8QuantConfig, Format
+
+    cfg4 = Float8QuantConfig(granularity=SG.BLOCKWISE, format=Format.E4M3, block_size=128)
+    a4g = a4.detach().requires_grad_(True)
+    w4g = w4.detach().requires_grad_(True)
+    gout4 = torch.randn((65536, 2048), generator=g).bfloat16().to(dev)
+
+    def step4():
+        a4g.grad = w4g.grad = None  # fresh gradients: no accumulation adds in the step
+        o = turbo.ops.grouped_gemm_fp8(a4g, w4g, lens, trans_b=True, config=cfg4)
+        o.backward(gout4)
+
+    res["cfg4_grouped_blockwise_moe_32x2048x7168"]["fwd_bwd_step"] = dict(
+        _gemm_rec(_time_settled(step4, max(5, it // 4)), 3 * 2.0 * 65536 * 2048 * 7168),
+        includes="quantize activation / weight / grad + grouped fwd + dgrad + variable-K wgrad")
+    del a4, w4, a4g, w4g, gout4
 
     # config 5: MX-FP8 (block 32, e8m0), Llama-3-70B up-proj 8192 x 8192 @ [28672 x 8192]^T
     sign = lambda t: torch.where(torch.rand(t, generator=g) < 0.5, -1.0, 1.0)  # noqa: E731
@@ -364,7 +382,36 @@ def _other_configs(args):
                                                          _mx_strides(ea5), False, ew5, _mx_strides(ew5), False,
                                                          out=o5), it), 2.0 * 8192 * 28672 * 8192),
     }
-    del a5, w5, qa5, qw5, o5
+    del qa5, qw5, o5
+    # second shape: down-proj x[8192, 28672] @ W[8192, 28672]^T (K = 28672)
+    x5 = (sign((8192, 28672)) * torch.exp(torch.randn((8192, 28672), generator=g) * 1.5)).bfloat16().to(dev)
+    wd5 = (sign((8192, 28672)) * torch.exp(torch.randn((8192, 28672), generator=g) * 1.5)).bfloat16().to(dev)
+    qx5, ex5 = quantize_mxfp8_impl(x5, e4, 1, 32, exp_kmajor=True)
+    qd5, ed5 = quantize_mxfp8_impl(wd5, e4, 1, 32, exp_kmajor=True)
+    od5 = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
+    res["cfg5_mxfp8_8192x28672x8192_NT"]["gemm_down_8192x8192x28672"] = _gemm_rec(
+        _time_settled(lambda: gemm_fp8_nt(qx5, qd5, torch.bfloat16, SG.MX_BLOCKWISE, ex5, _mx_strides(ex5), False,
+                                          ed5, _mx_strides(ed5), False, out=od5), it), 2.0 * 8192 * 8192 * 28672)
+    del x5, wd5, qx5, qd5, od5
+    # the up-proj layer step through the public op, HYBRID format (e4m3 forward, e5m2 gradient)
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import Float8QuantConfig, Format, ScaleDtype
+
+    cfg5 = Float8QuantConfig(granularity=SG.MX_BLOCKWISE, format=Format.HYBRID, block_size=32,
+                             scale_dtype=ScaleDtype.E8M0)
+    a5g = a5.detach().requires_grad_(True)
+    w5g = w5.detach().requires_grad_(True)
+    gout5 = torch.randn((8192, 28672), generator=g).bfloat16().to(dev)
+
+    def step5():
+        a5g.grad = w5g.grad = None
+        o = turbo.ops.gemm_fp8(a5g, w5g, False, True, torch.bfloat16, cfg5)
+        o.backward(gout5)
+
+    res["cfg5_mxfp8_8192x28672x8192_NT"]["fwd_bwd_step_hybrid"] = dict(
+        _gemm_rec(_time_settled(step5, max(5, it // 4)), 3 * 2.0 * 8192 * 28672 * 8192),
+        includes="MX dual quantize of activation / weight / grad + fwd + dgrad + wgrad")
+    del a5, w5, a5g, w5g, gout5
 
     # MoE token permutation producing config 4's operand shape: 8192 dispatched
     # tokens, each routed to 8 of the 32 local experts, hidden 7168 -> 65536

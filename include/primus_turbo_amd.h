@@ -115,18 +115,25 @@ int pta_quantize_fp8_blockwise_for_weight(const void *w, int in_dtype, int64_t B
                                           int64_t N, int64_t block, void *q, float *s, void *q_t,
                                           int fmt, pta_stream_t stream);
 
+/* layout flag of pta_quantize_fp8_blockwise_segment_m_row_col: q_col_pad is
+ * written transposed, [N, roundup(M, 128) + 128 * G] (column m = padded row m,
+ * zero bytes in padding rows), K-contiguous for the variable-K wgrad GEMM */
+#define PTA_SEGMENT_COL_TRANSPOSED 1
+
 /* Grouped segment row + col quant (block 128): rows of x[M, N] belong to G
  * groups (group_offs[G+1], device).  Produces q_row[M,N], s_row_t[ceil(N/128), M]
  * (transposed row scales), the 128-padded column-quantized q_col_pad[M+G*128, N]
- * with s_col_pad[ceil((M+G*128)/128), N], and vk_lens[G] / vk_offs[G+1]
- * (group lengths rounded up to 128 and their prefix sum).  All on device.
+ * (or its transpose, see PTA_SEGMENT_COL_TRANSPOSED) with
+ * s_col_pad[ceil((M+G*128)/128), N], and vk_lens[G] / vk_offs[G+1] (group
+ * lengths rounded up to 128 and their prefix sum).  All on device.
  * Replaces quantize_fp8_blockwise_segment_m_row_col (quantization.cpp:1382-1439). */
 int pta_quantize_fp8_blockwise_segment_m_row_col(const void *x, int in_dtype, int64_t M,
                                                  int64_t N, int64_t G, const int64_t *group_lens,
                                                  const int64_t *group_offs, int64_t block,
                                                  void *q_row, void *q_col_pad, float *s_row_t,
                                                  float *s_col_pad, int64_t *vk_lens,
-                                                 int64_t *vk_offs, int fmt, pta_stream_t stream);
+                                                 int64_t *vk_offs, int fmt, int layout,
+                                                 pta_stream_t stream);
 
 /* Exponent layout of pta_quantize_mxfp8: 0 = [rows, cols_pad/32] (the
  * reference's); PTA_MX_EXP_KMAJOR = K-block major [cols_pad/128][rows][4]: the
@@ -320,13 +327,17 @@ int pta_grouped_gemm_fp8_variable_k(const void *lhs, int lhs_fmt, const void *lh
                                     size_t workspace_bytes, pta_stream_t stream);
 
 /* Variable-K grouped GEMM on operands already transposed and padded per
- * group (MX wgrad): out[g] = op_c( lhs_t[:, seg_g] @ rhs_t[:, seg_g]^T ) with
+ * group (wgrad): out[g] = op_c( lhs_t[:, seg_g] @ rhs_t[:, seg_g]^T ) with
  * lhs_t[OUT_M, K_pad], rhs_t[OUT_N, K_pad], seg_g = columns
- * [group_offs[g], group_offs[g+1]) (multiples of 128), E8M0 scales
- * lhs_scale[OUT_M, K_pad/32], rhs_scale[OUT_N, K_pad/32]; out[G, OUT_M, OUT_N]
+ * [group_offs[g], group_offs[g+1]) (multiples of 128); out[G, OUT_M, OUT_N]
  * (trans_c = 0) or [G, OUT_N, OUT_M].  Empty groups give zero slices.
+ * Scales: MX_BLOCKWISE E8M0 lhs_scale[OUT_M, K_pad/32], rhs_scale[OUT_N, K_pad/32];
+ * BLOCKWISE fp32 lhs_scale[K_pad/128, OUT_M], rhs_scale[K_pad/128, OUT_N]
+ * (the segment quant's column scales).
  * Replaces the MX call of grouped_gemm_fp8_variable_k_impl
- * (primus_turbo/pytorch/ops/grouped_gemm_fp8.py:760-775). */
+ * (primus_turbo/pytorch/ops/grouped_gemm_fp8.py:760-775) and, for BLOCKWISE,
+ * grouped_gemm_fp8_variable_k_impl on the segment quant's column copies
+ * (grouped_gemm_fp8.py:186-200) without transposing them first. */
 int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt, const void *lhs_scale,
                                        const void *rhs_t, int rhs_fmt, const void *rhs_scale,
                                        const int64_t *group_offs, int64_t G, int64_t K_pad,

@@ -21,4 +21,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char *pta_last_error(void) { return pta::g_last_error; }
 
-extern "C" int pta_abi_version(void) { return 4; }
+extern "C" int pta_abi_version(void) { return 5; }

@@ -259,7 +259,7 @@ extern "C" int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt
                                                   int trans_c, int granularity, pta_stream_t stream) {
     clear_error();
     const int sm = gran_sm(granularity);
-    PTA_CHECK_ARG(sm == SM_MX, "the pre-transposed variable-K entry supports MX_BLOCKWISE");
+    PTA_CHECK_ARG(sm == SM_MX || sm == SM_BLOCK, "the pre-transposed variable-K entry supports MX_BLOCKWISE and BLOCKWISE");
     PTA_CHECK_ARG(lhs_t && rhs_t && out && lhs_scale && rhs_scale && group_offs, "NULL pointer argument");
     PTA_CHECK_ARG(G >= 1 && G <= 65535 && K_pad >= 0 && OUT_M >= 0 && OUT_N >= 0, "bad shape");
     PTA_CHECK_ARG(K_pad % 128 == 0, "K_pad must be a multiple of 128");
@@ -269,8 +269,9 @@ extern "C" int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt
     hipStream_t  st = as_stream(stream);
     const size_t eb = c_dtype == PTA_F32 ? 4 : 2;
     // NT problem per group: C[m, n] = sum_{k in segment g} lhs_t[m, k] rhs_t[n, k];
-    // segment offsets are multiples of 128, so the exponent index of K block
-    // kb is 4 * kb + (0..3) in the padded layout
+    // segment offsets are multiples of 128, so K block kb of a segment is
+    // global K block (offset / 128 + kb) of the padded layout: the exponent
+    // bytes 4 kb + (0..3) (MX) or the scale row kb (blockwise column scales)
     GemmArgs   g{};
     const bool swap = trans_c != 0;
     g.a = static_cast<const uint8_t *>(swap ? rhs_t : lhs_t);
@@ -278,8 +279,13 @@ extern "C" int pta_grouped_gemm_fp8_variable_k_nt(const void *lhs_t, int lhs_fmt
     g.M = swap ? OUT_N : OUT_M; g.N = swap ? OUT_M : OUT_N; g.K = K_pad;
     g.lda = K_pad; g.ldb = K_pad; g.ldc = g.N;
     g.sa = swap ? rhs_scale : lhs_scale; g.sb = swap ? lhs_scale : rhs_scale;
-    g.sa_m = K_pad / 32; g.sb_m = K_pad / 32; g.sa_k = 4; g.sb_k = 4;
-    g.sa_bytes = g.M * (K_pad / 32); g.sb_bytes = g.N * (K_pad / 32);
+    if (sm == SM_MX) {
+        g.sa_m = K_pad / 32; g.sb_m = K_pad / 32; g.sa_k = 4; g.sb_k = 4;
+        g.sa_bytes = g.M * (K_pad / 32); g.sb_bytes = g.N * (K_pad / 32);
+    } else { // fp32 [K_pad/128, rows]
+        g.sa_m = 1; g.sa_k = g.M; g.sa_bytes = (K_pad / 128) * g.M * 4;
+        g.sb_m = 1; g.sb_k = g.N; g.sb_bytes = (K_pad / 128) * g.N * 4;
+    }
     g.group_mode = 2; g.group_offs = group_offs; g.G = G;
     g.c = out; g.c_gstride = OUT_M * OUT_N * static_cast<int64_t>(eb);
     g.aligned_c = ((g.N * static_cast<int64_t>(eb)) % 16 == 0) && aligned16(out);

@@ -39,6 +39,7 @@ struct QBArgs {
     float      *s_row;     // ROW: s_row[r * srow_m + kb * srow_k]
     int64_t     srow_m, srow_k;
     uint8_t    *q_col;     // COL output
+    int64_t     ldt_col;   // COL_T: row stride of the transposed q_col [N, ldt_col]
     float      *s_col;     // COL: [mb, N]
     uint8_t    *q_t;       // W2D_T output
     float      *s_w;       // W2D: [B, mb, nb]
@@ -268,9 +269,10 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 s_tr[cseg * 16 + j][rgrp] = packed;
             }
             __syncthreads();
-            // 128 output rows (n) x 128 bytes (m): 16-byte chunks; the row stride is
-            // M rounded up to 128 and the padding bytes (rows past M) are zero
-            const int64_t ldt = (M + TILE - 1) / TILE * TILE;
+            // 128 output rows (n) x 128 bytes (m): 16-byte chunks; the row stride
+            // ldt_col is a multiple of 128 and the padding bytes (rows past M, or
+            // past a group's rows in segment mode) are zero
+            const int64_t ldt = args.ldt_col;
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 const int     c   = it * NT + t;
@@ -507,6 +509,7 @@ extern "C" int pta_quantize_fp8_blockwise_dual(const void *x, int in_dtype, int6
     if (layout & PTA_DUAL_ROW_SCALE_KMAJOR) { a.srow_m = 1; a.srow_k = M; }
     else { a.srow_m = cdiv(N, TILE); a.srow_k = 1; }
     a.q_col = static_cast<uint8_t *>(q_col); a.s_col = s_col;
+    a.ldt_col = cdiv(M, TILE) * TILE;
     dim3       grid(static_cast<uint32_t>(cdiv(M, TILE)), static_cast<uint32_t>(cdiv(N, TILE)), 1);
     PTA_CHECK_ARG(!col_transposed || aligned16(q_col), "transposed q_col must be 16-byte aligned");
     const bool v = vec_ok(x, in_dtype, N, {q_row, col_transposed ? nullptr : q_col});
@@ -545,10 +548,11 @@ extern "C" int pta_quantize_fp8_blockwise_for_weight(const void *w, int in_dtype
 extern "C" int pta_quantize_fp8_blockwise_segment_m_row_col(
     const void *x, int in_dtype, int64_t M, int64_t N, int64_t G, const int64_t *group_lens,
     const int64_t *group_offs, int64_t block, void *q_row, void *q_col_pad, float *s_row_t,
-    float *s_col_pad, int64_t *vk_lens, int64_t *vk_offs, int fmt, pta_stream_t stream) {
+    float *s_col_pad, int64_t *vk_lens, int64_t *vk_offs, int fmt, int layout, pta_stream_t stream) {
     clear_error();
     if (int rc = check_common(x, in_dtype, fmt, block)) return rc;
     PTA_CHECK_ARG(M >= 0 && N >= 0 && G >= 1, "bad shape");
+    PTA_CHECK_ARG(layout == 0 || layout == PTA_SEGMENT_COL_TRANSPOSED, "unknown layout %d", layout);
     PTA_CHECK_ARG(group_lens && group_offs && vk_offs && vk_lens, "group arrays must be set");
     PTA_CHECK_ARG(q_row && q_col_pad && s_row_t && s_col_pad, "outputs must be set");
     hipStream_t st = as_stream(stream);
@@ -561,8 +565,16 @@ extern "C" int pta_quantize_fp8_blockwise_segment_m_row_col(
     a.q_row = static_cast<uint8_t *>(q_row); a.s_row = s_row_t;
     a.srow_m = 1; a.srow_k = M;
     a.q_col = static_cast<uint8_t *>(q_col_pad); a.s_col = s_col_pad;
+    a.ldt_col = cdiv(M, TILE) * TILE + G * TILE;
     a.group_offs = group_offs; a.padded_offs = vk_offs; a.G = G;
     dim3 grid(static_cast<uint32_t>(cdiv(M_pad_max, TILE)), static_cast<uint32_t>(cdiv(N, TILE)), 1);
+    if (layout == PTA_SEGMENT_COL_TRANSPOSED) {
+        // q_col [N, roundup(M, 128) + 128 G]: column m of the transposed copy is
+        // row m of the padded layout (16-byte chunks, zero padding rows)
+        PTA_CHECK_ARG(aligned16(q_col_pad), "transposed q_col must be 16-byte aligned");
+        const bool v = vec_ok(x, in_dtype, N, {q_row});
+        return launch_tile<QB_ROW | QB_COL | QB_COL_T | QB_SEGMENT>(a, in_dtype, fmt, grid, v, st);
+    }
     const bool v = vec_ok(x, in_dtype, N, {q_row, q_col_pad});
     return launch_tile<QB_ROW | QB_COL | QB_SEGMENT>(a, in_dtype, fmt, grid, v, st);
 }

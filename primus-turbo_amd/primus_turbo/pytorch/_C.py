@@ -21,6 +21,8 @@ PTA_TENSORWISE, PTA_ROWWISE, PTA_BLOCKWISE, PTA_MX_BLOCKWISE = 1, 2, 3, 4
 DUAL_COL_TRANSPOSED, DUAL_ROW_SCALE_KMAJOR = 1, 2
 # exponent layout flag of pta_quantize_mxfp8
 MX_EXP_KMAJOR = 1
+# layout flag of pta_quantize_fp8_blockwise_segment_m_row_col
+SEGMENT_COL_TRANSPOSED = 1
 # expert_map kinds of pta_moe_permute_preprocess
 MOE_MAP_BOOL, MOE_MAP_I32, MOE_MAP_I64 = 0, 1, 2
 
@@ -39,7 +41,7 @@ SIGNATURES = {
     "pta_quantize_fp8_blockwise_for_weight": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp]),
     "pta_quantize_fp8_blockwise_segment_m_row_col": (
         _i32,
-        [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp],
+        [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp],
     ),
     "pta_quantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "pta_dequantize_fp8_tensorwise": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp]),

@@ -105,20 +105,8 @@ def grouped_gemm_fp8_variable_k_impl(
     """
     gran = _gran_code(granularity)
     if gran == ScalingGranularity.MX_BLOCKWISE.value:
-        a = a.contiguous()
-        b = b.contiguous()
-        OUT_M, K_pad = a.shape
-        OUT_N = b.shape[0]
-        assert b.shape[1] == K_pad, "padded K mismatch"
-        G = group_lens.shape[0]
-        out = torch.empty((G, OUT_N, OUT_M) if trans_c else (G, OUT_M, OUT_N), dtype=out_dtype, device=a.device)
-        offs = group_offs.to(torch.int64).contiguous()
-        _C.call(
-            "pta_grouped_gemm_fp8_variable_k_nt", _C.ptr(a), _C.fp8_code(a.dtype), _C.ptr(_scale(a_scales, gran)),
-            _C.ptr(b), _C.fp8_code(b.dtype), _C.ptr(_scale(b_scales, gran)), _C.ptr(offs), G, K_pad, OUT_M, OUT_N,
-            _C.ptr(out), _C.out_dtype_code(out_dtype), int(trans_c), gran, _C.stream(a.device),
-        )
-        return out
+        return grouped_gemm_fp8_variable_k_nt_impl(a, b, a_scales, b_scales, group_lens.shape[0], group_offs,
+                                                   trans_c, out_dtype, gran)
     assert trans_a and not trans_b, "variable-K grouped GEMM expects trans_a=True, trans_b=False"
     a = a.contiguous()
     b = b.contiguous()
@@ -135,5 +123,37 @@ def grouped_gemm_fp8_variable_k_impl(
         _C.ptr(b), _C.fp8_code(b.dtype), _C.ptr(_scale(b_scales, gran)), _C.ptr(offs), G, M_total, OUT_M, OUT_N,
         _C.ptr(out), _C.out_dtype_code(out_dtype), int(trans_c), gran, int(num_cu or 0), _C.ptr(ws),
         0 if ws is None else ws.numel(), _C.stream(a.device),
+    )
+    return out
+
+
+def grouped_gemm_fp8_variable_k_nt_impl(
+    a_t: torch.Tensor,
+    b_t: torch.Tensor,
+    a_scales: torch.Tensor,
+    b_scales: torch.Tensor,
+    G: int,
+    padded_offs: torch.Tensor,
+    trans_c: bool,
+    out_dtype: torch.dtype,
+    granularity: int,
+) -> torch.Tensor:
+    """out[g] = a_t[:, seg_g] @ b_t[:, seg_g]^T (transposed with trans_c) on
+    column copies already transposed and padded per group: a_t [OUT_M, K_pad],
+    b_t [OUT_N, K_pad], seg_g = columns [padded_offs[g], padded_offs[g+1])
+    (multiples of 128).  MX: E8M0 scales [OUT_*, K_pad/32]; BLOCKWISE: the
+    segment quant's column scales [K_pad/128, OUT_*].  Empty groups give zeros."""
+    gran = _gran_code(granularity)
+    a_t = a_t.contiguous()
+    b_t = b_t.contiguous()
+    OUT_M, K_pad = a_t.shape
+    OUT_N = b_t.shape[0]
+    assert b_t.shape[1] == K_pad, "padded K mismatch"
+    out = torch.empty((G, OUT_N, OUT_M) if trans_c else (G, OUT_M, OUT_N), dtype=out_dtype, device=a_t.device)
+    offs = padded_offs.to(torch.int64).contiguous()
+    _C.call(
+        "pta_grouped_gemm_fp8_variable_k_nt", _C.ptr(a_t), _C.fp8_code(a_t.dtype), _C.ptr(_scale(a_scales, gran)),
+        _C.ptr(b_t), _C.fp8_code(b_t.dtype), _C.ptr(_scale(b_scales, gran)), _C.ptr(offs), G, K_pad, OUT_M, OUT_N,
+        _C.ptr(out), _C.out_dtype_code(out_dtype), int(trans_c), gran, _C.stream(a_t.device),
     )
     return out

@@ -235,12 +235,16 @@ def quant_fp8_blockwise_segment_m_row_col_impl(
     group_lens: torch.Tensor,
     group_offs: torch.Tensor,
     gemm_other_dim: Optional[int] = None,
+    col_transposed: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Fused row + segment-padded column quantization of a grouped tensor.
 
     Returns (x_fp8_row [M,N], x_fp8_col_padded [M+G*bs, N], x_scales_row [N/bs, M],
     x_scales_col_padded [(M+G*bs)/bs, N], var_k_group_lens [G], var_k_group_offs [G+1]).
     ``gemm_other_dim`` is accepted for signature compatibility; one kernel serves all sizes.
+    ``col_transposed=True`` (used by the grouped autograd function) returns the
+    column copy transposed, [N, roundup(M, 128) + G*bs]: the K-contiguous
+    operand of the variable-K wgrad GEMM, with no separate transpose pass.
     """
     _check_hp(x)
     assert x.is_contiguous() and x.dim() == 2
@@ -249,7 +253,10 @@ def quant_fp8_blockwise_segment_m_row_col_impl(
     Mpad = M + G * block_size
     dev = x.device
     q_row = torch.empty((M, N), dtype=dtype, device=dev)
-    q_col = torch.empty((Mpad, N), dtype=dtype, device=dev)
+    if col_transposed:
+        q_col = torch.empty((N, ceil_div(M, 128) * 128 + G * block_size), dtype=dtype, device=dev)
+    else:
+        q_col = torch.empty((Mpad, N), dtype=dtype, device=dev)
     s_row = torch.empty((ceil_div(N, block_size), M), dtype=torch.float32, device=dev)
     s_col = torch.empty((ceil_div(Mpad, block_size), N), dtype=torch.float32, device=dev)
     vk_lens = torch.empty(G, dtype=torch.int64, device=dev)
@@ -257,7 +264,8 @@ def quant_fp8_blockwise_segment_m_row_col_impl(
     _C.call(
         "pta_quantize_fp8_blockwise_segment_m_row_col", _C.ptr(x), _C.in_dtype_code(x.dtype), M, N, G,
         _C.ptr(group_lens.contiguous()), _C.ptr(group_offs.contiguous()), block_size, _C.ptr(q_row), _C.ptr(q_col),
-        _C.ptr(s_row), _C.ptr(s_col), _C.ptr(vk_lens), _C.ptr(vk_offs), _C.fp8_code(dtype), _C.stream(dev),
+        _C.ptr(s_row), _C.ptr(s_col), _C.ptr(vk_lens), _C.ptr(vk_offs), _C.fp8_code(dtype),
+        _C.SEGMENT_COL_TRANSPOSED if col_transposed else 0, _C.stream(dev),
     )
     return q_row, q_col, s_row, s_col, vk_lens, vk_offs
 

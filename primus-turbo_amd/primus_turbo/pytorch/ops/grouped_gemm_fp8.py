@@ -26,6 +26,7 @@ from primus_turbo.pytorch.core.quantized_tensor import (
 from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_fp8_impl import (
     grouped_gemm_fp8_impl,
     grouped_gemm_fp8_variable_k_impl,
+    grouped_gemm_fp8_variable_k_nt_impl,
 )
 from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
 from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
@@ -63,8 +64,9 @@ class FP8GroupedGemmBlockFunc(torch.autograd.Function):
         assert out_dtype in [torch.float16, torch.bfloat16]
         fdt = _get_fp8_dtype(config.format, True)
         bs = config.block_size
-        a_row, a_col, a_s_row, a_s_col, _, _ = quant_fp8_blockwise_segment_m_row_col_impl(
-            a.detach().contiguous(), fdt, bs, group_lens, group_offs
+        # column copy transposed ([K, M_pad], K-contiguous for the variable-K wgrad)
+        a_row, a_colT, a_s_row, a_s_col, _, _ = quant_fp8_blockwise_segment_m_row_col_impl(
+            a.detach().contiguous(), fdt, bs, group_lens, group_offs, col_transposed=True
         )
         b_fp8, b_s, b_fp8_t = quant_fp8_blockwise_for_weight_impl(b.detach().contiguous(), fdt, block_size=bs,
                                                                   with_transpose=True)
@@ -81,24 +83,31 @@ class FP8GroupedGemmBlockFunc(torch.autograd.Function):
             fwd_b, fwd_s, bwd_b, bwd_s = bt, b_t_s, b_fp8, b_s
         out = grouped_gemm_fp8_impl(a_row, fwd_b, a_s_row, fwd_s, group_lens, group_offs, False, True, out_dtype,
                                     config.granularity.value, num_cu)
-        ctx.save_for_backward(a_col, a_s_col, bwd_b, bwd_s, group_lens, group_offs)
+        ctx.save_for_backward(a_colT, a_s_col, bwd_b, bwd_s, group_lens, group_offs)
         ctx.trans_b, ctx.config, ctx.out_dtype, ctx.num_cu = trans_b, config, out_dtype, num_cu
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        a_col, a_s_col, bwd_b, bwd_s, group_lens, group_offs = ctx.saved_tensors
+        a_colT, a_s_col, bwd_b, bwd_s, group_lens, group_offs = ctx.saved_tensors
         bs = ctx.config.block_size
         gdt = _get_fp8_dtype(ctx.config.format, False)
-        g_row, g_col, g_s_row, g_s_col, vk_lens, vk_offs = quant_fp8_blockwise_segment_m_row_col_impl(
-            grad_out.contiguous(), gdt, bs, group_lens, group_offs
+        g_row, g_colT, g_s_row, g_s_col, vk_lens, vk_offs = quant_fp8_blockwise_segment_m_row_col_impl(
+            grad_out.contiguous(), gdt, bs, group_lens, group_offs, col_transposed=True
         )
         # dgrad: grad_a[m, k] = sum_n grad_out[m, n] b[g](n, k), NT on rows k
         grad_a = grouped_gemm_fp8_impl(g_row, bwd_b, g_s_row, bwd_s, group_lens, group_offs, False, True,
                                        ctx.out_dtype, ctx.config.granularity.value, ctx.num_cu)
-        grad_b = grouped_gemm_fp8_variable_k_impl(a_col, g_col, a_s_col, g_s_col, vk_lens, vk_offs, True, False,
-                                                  ctx.trans_b, ctx.out_dtype, ctx.config.granularity.value,
-                                                  ctx.num_cu)
+        # wgrad over each group's 128-padded rows, NT on the transposed column copies:
+        # dW[g] [N, K] = g_colT[:, seg] . a_colT[:, seg]^T (or [K, N] for trans_b=False)
+        G = group_lens.shape[0]
+        gran = ctx.config.granularity.value
+        if ctx.trans_b:
+            grad_b = grouped_gemm_fp8_variable_k_nt_impl(g_colT, a_colT, g_s_col, a_s_col, G, vk_offs, False,
+                                                         ctx.out_dtype, gran)
+        else:
+            grad_b = grouped_gemm_fp8_variable_k_nt_impl(a_colT, g_colT, a_s_col, g_s_col, G, vk_offs, False,
+                                                         ctx.out_dtype, gran)
         return grad_a, grad_b, None, None, None, None, None, None
 
 

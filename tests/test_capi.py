@@ -42,7 +42,7 @@ def test_argument_errors_raise_without_gpu():
     from primus_turbo.pytorch import _C
 
     lib = _C.load()
-    assert lib.pta_abi_version() == 4
+    assert lib.pta_abi_version() == 5
     # NULL input: rejected on the host before any HIP call
     rc = lib.pta_quantize_fp8_blockwise(None, 2, 128, 128, 128, 1, None, None, 0, None)
     assert rc == -1

@@ -249,6 +249,31 @@ def test_segment_vs_oracle_and_reference(lens, qdt):
         assert_f32_bitexact(f32(sc)[: P // 128], f32(sc2)[: P // 128], "col scales vs reference kernel")
 
 
+@pytest.mark.parametrize("lens", [[100, 0, 300, 128, 5], [0, 0, 64], [1000]])
+@pytest.mark.parametrize("N", [384, 200])
+def test_segment_col_transposed_vs_oracle(lens, N):
+    """The transposed column copy [N, roundup(M,128) + 128 G] holds the padded
+    column layout's rows as columns (the wgrad operand layout)."""
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import quant_fp8_blockwise_segment_m_row_col_impl
+
+    qdt = torch.float8_e4m3fn
+    M = sum(lens)
+    x = _input((max(M, 1), N), seed=11)[:M].contiguous()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = group_offs_from_lens(gl)
+    qr, qcT, sr, sc, vl, vo = quant_fp8_blockwise_segment_m_row_col_impl(x.cuda(), qdt, 128, gl, go,
+                                                                         col_transposed=True)
+    o = O.quant_block_segment(x, FMT[qdt], lens)
+    P = int(o[5][-1])
+    assert tuple(qcT.shape) == (N, (M + 127) // 128 * 128 + 128 * len(lens))
+    np.testing.assert_array_equal(vo.cpu().numpy(), o[5])
+    assert_bytes_equal(u8(qr), o[0], "row bytes")
+    assert_f32_bitexact(f32(sr), o[2], "row scales (transposed)")
+    assert_bytes_equal(u8(qcT)[:, :P], np.ascontiguousarray(o[1][:P].T), "transposed col bytes")
+    assert_f32_bitexact(f32(sc)[: P // 128], o[3][: P // 128], "col scales")
+
+
 # ---------------------------------------------------------------------------
 # MXFP8 (rule restated from the OCP MX spec; the reference kernel is absent)
 # ---------------------------------------------------------------------------
