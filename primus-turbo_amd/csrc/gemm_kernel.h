@@ -191,6 +191,25 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Longest-first order of the variable-K groups (grouped mode 2): workgroup
+// row r (blockIdx.y) takes the group with the r-th largest K segment (ties by
+// index), so the longest groups start first and the short ones fill the tail
+// instead of one long group running alone at the end.  Lane q holds group q's
+// length; its rank counts the groups ahead of it, read back with readlane.
+// Up to 64 groups (a rank costs G steps); beyond that the natural order.
+__device__ __forceinline__ int64_t longest_first_group(const int64_t *offs, int64_t G, int64_t r) {
+    if (G > 64) return r;
+    const int lane = threadIdx.x & 63;
+    const int kq   = lane < G ? static_cast<int>(offs[lane + 1] - offs[lane]) : -1;
+    int       rank = 0;
+    for (int p = 0; p < static_cast<int>(G); ++p) {
+        const int kp = __builtin_amdgcn_readlane(kq, p);
+        rank += (kp > kq) || (kp == kq && p < lane);
+    }
+    const uint64_t hit = __ballot(lane < G && rank == static_cast<int>(r));
+    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__builtin_ctzll(hit)));
+}
+
 // Group of M-tile row `mt` in grouped mode 1: the wave computes every group's
 // tile count (ceil(rows / BM)) and their prefix sums 64 groups at a time and
 // picks the group whose tile range holds `mt` with one ballot.  Returns -1
@@ -286,8 +305,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
         const int tile_n    = (id % per_group) / gsz;
         m0 = static_cast<int64_t>(tile_m) * BM;
         n0 = static_cast<int64_t>(tile_n) * BN_;
-        if (g.group_mode == 2) {
-            const int64_t q  = blockIdx.y;
+        // the persistent form serves dense and M-grouped problems only
+        if (!PERSIST && g.group_mode == 2) {
+            const int64_t q  = longest_first_group(g.group_offs, g.G, blockIdx.y);
             const int64_t k0 = g.group_offs[q];
             K       = g.group_offs[q + 1] - k0;
             A       = g.a + k0;
