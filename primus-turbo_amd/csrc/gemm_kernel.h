@@ -270,12 +270,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
     int64_t        kb_base = 0; // first global K block of this problem (group_mode 2)
     if (g.group_mode == 1) {
         // XCD-aware order: workgroups are dispatched round-robin over the 8
-        // XCDs, so XCD x takes M-tile rows x, x + 8, ... each with all of the
-        // row's N-tiles, and a row's A tile is fetched into one XCD's L2 only
-        // (tiles_m is a multiple of 8 in this mode; surplus rows exit below).
-        const int64_t b8 = bid >> 3;
-        const int64_t id = (8 * (b8 / g.tiles_n) + (bid & 7)) * g.tiles_n + b8 % g.tiles_n;
-        const int64_t mt = id / g.tiles_n, tn = id % g.tiles_n;
+        // XCDs.  M-tile rows go in blocks of 32: XCD x takes rows 4x .. 4x+3
+        // of each block and walks their N-tiles four rows at a time, so the
+        // tiles one XCD runs together share A rows (8 N-tiles each) and B
+        // tiles (4 rows each, of one group's B) in its L2.  tiles_m is a
+        // multiple of 32 in this mode; surplus rows exit below.
+        const int64_t b8  = bid >> 3;
+        const int64_t per = 4 * g.tiles_n; // slots of one XCD's 4-row block
+        const int64_t w   = b8 % per;
+        const int64_t mt  = (b8 / per) * 32 + (bid & 7) * 4 + (w & 3);
+        const int64_t tn  = w >> 2;
         int64_t       cum = 0, gstart = 0, gend = 0;
         const int64_t grp = find_tile_group(g.group_offs, g.G, mt, cum, gstart, gend);
         if (grp < 0) return; // past the last tile (the tile count is an upper bound)

@@ -167,11 +167,11 @@ extern "C" int pta_grouped_gemm_fp8(const void *a, int a_fmt, const void *a_scal
         g.sa_bytes = 4; g.sb_bytes = 4; g.sb_gstride = 0; // one scalar shared by all groups
     }
     // tile-list upper bound: every group may add one partial tile; rows rounded
-    // up to a multiple of 8 for the kernel's XCD-aware tile order.  Persistent
+    // up to a multiple of 32 for the kernel's XCD-aware tile order.  Persistent
     // grid: one workgroup per CU (the tile uses most of a CU's LDS), or
     // num_cu of them, which leaves the other CUs free for concurrent work.
     g.tiles_n    = static_cast<int>(cdiv(N, BN));
-    g.tiles_m    = static_cast<int>(cdiv(cdiv(M_total, BM) + G, 8) * 8);
+    g.tiles_m    = static_cast<int>(cdiv(cdiv(M_total, BM) + G, 32) * 32);
     const int cu = cu_count();
     g.persistent = num_cu > 0 && num_cu < cu ? num_cu : cu;
     if (int rc = run(g, sm, false, b2d, a_fmt, b_fmt, c_dtype, st)) return rc;
