@@ -116,6 +116,45 @@ def test_grouped_variable_k_blockwise_vs_oracle(lens, trans_c):
         _check(o[g], ref, f"group {g}")
 
 
+def _lens_many(G, seed):
+    gen = torch.Generator().manual_seed(seed)
+    lens = torch.randint(0, 400, (G,), generator=gen)
+    lens[torch.randperm(G, generator=gen)[: G // 4]] = 0
+    return [int(v) for v in lens]
+
+
+@pytest.mark.parametrize("lens", [[300, 0, 513, 128, 59, 128, 128, 0], [0, 0, 0, 1], _lens_many(64, 1),
+                                  _lens_many(70, 2)])
+def test_variable_k_pretransposed_equals_transposing_entry(lens):
+    """The wgrad the autograd function runs (K-contiguous column copies from
+    the segment quant, groups taken longest-K first for G <= 64, in order
+    beyond) gives the same bits as the transposing variable-K entry on the
+    row-major padded copies; ties, empty groups and G > 64 included."""
+    (turbo, _, _, SG, _, _, gvk, offs_from, segq) = _mods()
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_fp8_impl import grouped_gemm_fp8_variable_k_nt_impl
+
+    G, K, N = len(lens), 384, 256
+    M = sum(lens)
+    a = randn((max(M, 1), K), seed=15).cuda()[:M].contiguous()
+    gout = randn((max(M, 1), N), seed=16).cuda()[:M].contiguous()
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = offs_from(gl)
+    qdt = torch.float8_e4m3fn
+    _, a_col, _, a_s_col, vl, vo = segq(a, qdt, 128, gl, go)
+    _, g_col, _, g_s_col, _, _ = segq(gout, qdt, 128, gl, go)
+    _, a_colT, _, a_s_colT, _, vo2 = segq(a, qdt, 128, gl, go, col_transposed=True)
+    _, g_colT, _, g_s_colT, _, _ = segq(gout, qdt, 128, gl, go, col_transposed=True)
+    assert torch.equal(vo, vo2)
+    ref = gvk(a_col, g_col, a_s_col, g_s_col, vl, vo, True, False, False, torch.bfloat16, SG.BLOCKWISE.value)
+    out = grouped_gemm_fp8_variable_k_nt_impl(a_colT, g_colT, a_s_colT, g_s_colT, G, vo2, False, torch.bfloat16,
+                                              SG.BLOCKWISE.value)
+    assert out.shape == (G, K, N)
+    assert torch.equal(out, ref)
+    outT = grouped_gemm_fp8_variable_k_nt_impl(g_colT, a_colT, g_s_colT, a_s_colT, G, vo2, True, torch.bfloat16,
+                                               SG.BLOCKWISE.value)
+    assert torch.equal(outT, ref)
+
+
 @pytest.mark.parametrize("lens", [[300, 0, 513, 128, 59], [64, 64, 64, 64]])
 @pytest.mark.parametrize("gran", ["BLOCKWISE", "TENSORWISE", "ROWWISE", "MX_BLOCKWISE"])
 def test_grouped_gemm_fp8_autograd(lens, gran):
