@@ -581,7 +581,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
 #pragma unroll 4
             for (int q = 0; q < BM / RPP; ++q) {
                 const int r = t / CH + RPP * q;
-                *reinterpret_cast<uint4 *>(Cb + r * g.ldc) = *reinterpret_cast<const uint4 *>(smem + r * EPITCH_ + c16 * 16);
+                // non-temporal: C is not read again by this launch (measured:
+                // headline -1.4%, grouped dgrad -2.4%, no case slower)
+                typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+                __builtin_nontemporal_store(*reinterpret_cast<const v4u *>(smem + r * EPITCH_ + c16 * 16),
+                                            reinterpret_cast<v4u *>(Cb + r * g.ldc));
             }
             return;
         }
