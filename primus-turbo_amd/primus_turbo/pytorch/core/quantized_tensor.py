@@ -275,6 +275,8 @@ class QuantizedTensor(torch.Tensor):
                 self._data, self._orig_dtype, g, block_size=self._block_size, axis=self.quantized_axis,
                 scale_inv=self._scale_inv, scaling_recipe=self._scaling_recipe,
             )
+            if g == ScalingGranularity.MX_BLOCKWISE and out.dim() == 3 and self.quantized_axis == 1:
+                out = out.transpose(1, 2)  # 3-D colwise MX dequantizes in the stored [B, N, M_pad] layout
         # MX outputs carry the 128-padding of the stored layout
         return out[..., : self.shape[-2], : self.shape[-1]].contiguous()
 

@@ -454,7 +454,10 @@ def grouped_quantize_mxfp8_impl(
 def dequantize_mxfp8_impl(
     x: torch.Tensor, out_dtype: torch.dtype, axis: int, block_size: int, scale_inv: torch.Tensor
 ) -> torch.Tensor:
-    """Rowwise (axis 1 / 2): y[M, N_pad]; colwise (axis 0 / 1 of 3D): y = transpose of q[N, M_pad]."""
+    """Rowwise (axis 1 / 2): y has q's shape.  Colwise 2-D (axis 0): y[M_pad, N]
+    = the transpose of q[N, M_pad].  Colwise 3-D (axis 1): y keeps q's layout
+    [B, N, M_pad], as the reference's dequantize_mxfp8 returns it
+    (quantization.cpp:283-357: a [B, N, M_pad] permutation of its output)."""
     assert x.is_contiguous(), "The x tensor must be contiguous."
     assert x.dim() in (2, 3), "The x must be a 2D or 3D tensor."
     assert scale_inv.dim() == x.dim(), "The scale_inv rank must match x."
@@ -475,13 +478,14 @@ def dequantize_mxfp8_impl(
             _C.out_dtype_code(out_dtype), _C.stream(x.device),
         )
         return y
+    # 3-D: every row of q[B, R, C] carries its own exponents in both directions,
+    # and neither direction transposes the result, so one launch over B * R rows
     G, R, C = x.shape
-    y = torch.empty((G, R, C) if rowwise else (G, C, R), dtype=out_dtype, device=x.device)
-    for g in range(G):
-        _C.call(
-            "pta_dequantize_mxfp8", _C.ptr(x[g]), _C.fp8_code(x.dtype), R, C, _C.ptr(e[g]), int(not rowwise),
-            _C.ptr(y[g]), _C.out_dtype_code(out_dtype), _C.stream(x.device),
-        )
+    y = torch.empty((G, R, C), dtype=out_dtype, device=x.device)
+    _C.call(
+        "pta_dequantize_mxfp8", _C.ptr(x), _C.fp8_code(x.dtype), G * R, C, _C.ptr(e), 0, _C.ptr(y),
+        _C.out_dtype_code(out_dtype), _C.stream(x.device),
+    )
     return y
 
 
@@ -647,9 +651,8 @@ def _mx_fake_flat(x, out_dtype, axis, block_size, with_trans, use_2d_row, shuffl
 
 
 def _mx_deq_fake(x, out_dtype, axis, block_size, scale_inv):
-    rowwise = axis == (1 if x.dim() == 2 else 2)
     shape = list(x.shape)
-    if not rowwise:
+    if x.dim() == 2 and axis == 0:  # 2-D colwise transposes back; 3-D keeps q's layout
         shape[-1], shape[-2] = shape[-2], shape[-1]
     return torch.empty(shape, dtype=out_dtype, device=x.device)
 

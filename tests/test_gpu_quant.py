@@ -392,3 +392,39 @@ def test_reference_roundtrip_tolerance():
         q, s = turbo.ops.quantize_fp8(x, torch.float8_e4m3fn, g, **kw)
         y = turbo.ops.dequantize_fp8(q, torch.bfloat16, g, scale_inv=s, **kw)
         torch.testing.assert_close(y, x, rtol=0.1, atol=0.1)
+
+
+def _mx_padded_ref(x, axis, align=128):
+    """Zero-padded input in the layout MX dequantize returns (the reference's
+    mxfp8_padded_ref, tests/pytorch/ops/test_quantization.py:252-275)."""
+    pad = lambda n: (align - n % align) % align  # noqa: E731
+    if x.dim() == 2:
+        if axis == 0:
+            return torch.cat([x, torch.zeros(pad(x.size(0)), x.size(1), dtype=x.dtype, device=x.device)], 0)
+        return torch.cat([x, torch.zeros(x.size(0), pad(x.size(1)), dtype=x.dtype, device=x.device)], 1)
+    if axis == 1:
+        xt = x.transpose(1, 2).contiguous()
+        return torch.cat([xt, torch.zeros(xt.size(0), xt.size(1), pad(xt.size(2)), dtype=x.dtype, device=x.device)], 2)
+    return torch.cat([x, torch.zeros(x.size(0), x.size(1), pad(x.size(2)), dtype=x.dtype, device=x.device)], 2)
+
+
+@pytest.mark.parametrize("orig_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dest_dtype", FP8)
+@pytest.mark.parametrize("batched", [False, True])
+@pytest.mark.parametrize("MN", [(32, 256), (256, 64), (1024, 32)])
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("use_2d_block", [True, False])
+def test_reference_mx_roundtrip(orig_dtype, dest_dtype, batched, MN, axis, use_2d_block):
+    """The reference's MXFP8 criterion (test_quantization.py:302-357): quantize
+    along `axis`, dequantize, and compare with the zero-padded input at the
+    fp8 tolerance of tests/pytorch/test_utils.py:17-31 (rtol = atol = 0.1)."""
+    turbo, SG, SR = _turbo()
+    M, N = MN
+    torch.manual_seed(42)
+    x = torch.randn((3, M, N) if batched else (M, N), device="cuda", dtype=orig_dtype)
+    qaxis = axis + 1 if batched else axis
+    rec = SR(use_2d_block=use_2d_block)
+    q, s = turbo.ops.quantize_fp8(x, dest_dtype, SG.MX_BLOCKWISE, axis=qaxis, block_size=32, scaling_recipe=rec)
+    y = turbo.ops.dequantize_fp8(q, orig_dtype, SG.MX_BLOCKWISE, block_size=32, axis=qaxis, scale_inv=s,
+                                 scaling_recipe=rec)
+    torch.testing.assert_close(_mx_padded_ref(x, qaxis), y, rtol=0.1, atol=0.1)

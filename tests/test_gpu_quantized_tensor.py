@@ -78,6 +78,19 @@ def test_transposes():
     assert torch.equal(t.scale_inv, ref.scale_inv)
 
 
+def test_batched_colwise_mx_quantized_tensor():
+    """3-D MX along the middle axis: dequantize() gives the original [B, M, N]
+    back (the op itself returns the stored [B, N, M_pad] layout)."""
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity as SG, ScalingRecipe as SR
+    from primus_turbo.pytorch.core.quantized_tensor import QuantizedTensor as QT
+
+    x = torch.randn((2, 96, 64), generator=torch.Generator().manual_seed(4)).bfloat16().cuda()
+    q = QT.quantize(x, torch.float8_e4m3fn, SG.MX_BLOCKWISE, axis=-2, block_size=32, scaling_recipe=SR())
+    y = q.dequantize()
+    assert y.shape == x.shape
+    torch.testing.assert_close(y, x, rtol=0.1, atol=0.1)
+
+
 @pytest.mark.parametrize("axis", [-1, -2])
 def test_grouped_mx_quantized_tensor(axis):
     """Grouped MX QuantizedTensor: padded groups in, packed rows back out of
