@@ -46,6 +46,13 @@ int gran_to_sm(int gran) {
     default: return -1;
     }
 }
+
+// zero fill of an empty-K product (a kernel, not a memset, so that it may be
+// recorded into a graph)
+__global__ void zero_fill_kernel(uint8_t *c, int64_t bytes) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes; i += stride) c[i] = 0;
+}
 } // namespace
 
 extern "C" size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, int trans_a,
@@ -79,7 +86,8 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
     hipStream_t st = as_stream(stream);
     if (K == 0) {
         const size_t eb = c_dtype == PTA_F32 ? 4 : 2;
-        PTA_CHECK_HIP(hipMemsetAsync(c, 0, static_cast<size_t>(M * N) * eb, st));
+        zero_fill_kernel<<<256, 256, 0, st>>>(static_cast<uint8_t *>(c), M * N * static_cast<int64_t>(eb));
+        PTA_CHECK_LAUNCH();
         return PTA_OK;
     }
     const size_t need = pta_gemm_fp8_workspace_size(M, N, K, trans_a, trans_b, granularity);

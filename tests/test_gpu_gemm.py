@@ -279,3 +279,20 @@ def test_float8_linear_fwd_bwd(gran):
         s = O.snr_db(f32(r), f32(a))
         assert s > 25, f"{name} SNR {s:.1f} dB"
     assert lin.weight.grad is not None and lin.weight.grad.shape == lin.weight.shape
+
+
+def test_empty_k_writes_zeros():
+    """K = 0: the product is a zero matrix, written by a fill kernel (no memset,
+    so the call can be recorded into a graph)."""
+    from primus_turbo.pytorch import _C
+
+    M, N = 300, 200
+    a = torch.empty((M, 16), dtype=torch.float8_e4m3fn, device="cuda")
+    b = torch.empty((N, 16), dtype=torch.float8_e4m3fn, device="cuda")
+    s = torch.ones((), dtype=torch.float32, device="cuda")
+    out = torch.full((M, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    _C.call("pta_gemm_fp8", _C.ptr(a), _C.fp8_code(a.dtype), _C.ptr(s), 0, _C.ptr(b), _C.fp8_code(b.dtype),
+            _C.ptr(s), 1, _C.ptr(out), _C.out_dtype_code(out.dtype), 0, M, N, 0, _C.PTA_TENSORWISE, None, 0,
+            _C.stream(a.device))
+    torch.cuda.synchronize()
+    assert not out.float().any()

@@ -326,3 +326,77 @@ def test_grouped_gemm_many_groups():
             s = O.snr_db(f32(ref_g), f32(out[off:off + L]))
             assert s > 25, f"group {g_}: SNR {s:.1f} dB vs the fp32 product"
         off += L
+
+
+def test_blockwise_zero_group_lens_reference_case():
+    """The reference's regression case (test_grouped_gemm_fp8.py:1008-1068):
+    8 experts, only the first two receive tokens, K = 2048, N = 8192; forward
+    and both gradients above 25 dB against the bf16 autograd reference."""
+    (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
+    lens_l = [8192, 8192, 0, 0, 0, 0, 0, 0]
+    E, K, N = 8, 2048, 8192
+    gen = torch.Generator().manual_seed(0)
+    a = torch.randn((sum(lens_l), K), generator=gen).bfloat16().cuda().requires_grad_()
+    b = torch.randn((E, N, K), generator=gen).bfloat16().cuda().requires_grad_()
+    gl = torch.tensor(lens_l, dtype=torch.int64, device="cuda")
+    cfg = Cfg(format=Format.E4M3, granularity=SG.BLOCKWISE, block_size=128)
+    out = turbo.ops.grouped_gemm_fp8(a, b, gl, trans_b=True, config=cfg)
+    grad = torch.randn(out.shape, generator=gen).bfloat16().cuda()
+    out.backward(grad)
+    a_ref = a.detach().float().requires_grad_()
+    b_ref = b.detach().float().requires_grad_()
+    ref = torch.cat([a_ref[:8192] @ b_ref[0].T, a_ref[8192:] @ b_ref[1].T])
+    ref.backward(grad.float())
+    assert out.shape == ref.shape and a.grad.shape == a_ref.grad.shape and b.grad.shape == b_ref.grad.shape
+    for name, x, r in (("out", out, ref), ("dA", a.grad, a_ref.grad), ("dB", b.grad, b_ref.grad)):
+        s = O.snr_db(f32(r), f32(x))
+        assert s > 25, f"{name} SNR {s:.1f} dB"
+    assert not b.grad[2:].float().any(), "experts without tokens get zero weight gradients"
+
+
+@pytest.mark.parametrize("gran", ["BLOCKWISE", "TENSORWISE"])
+def test_grouped_layer_graph_replay(gran):
+    """Forward + backward of grouped_gemm_fp8 recorded once into a HIP graph and
+    replayed with the group sizes changed in place (the reference's hipgraph
+    scenario, test_grouped_gemm_fp8.py:800-925): every replay, with eager work
+    and synchronisations between replays, gives the same bits as an eager call
+    with those sizes.  Group sizes live on the device, so nothing is re-planned
+    on the host."""
+    (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
+    G, K, N = 4, 512, 256
+    lens1 = torch.tensor([300, 0, 500, 224], dtype=torch.int64, device="cuda")
+    lens2 = torch.tensor([100, 600, 0, 324], dtype=torch.int64, device="cuda")
+    M = int(lens1.sum())
+    gen = torch.Generator().manual_seed(5)
+    a = torch.randn((M, K), generator=gen).bfloat16().cuda().requires_grad_()
+    b = torch.randn((G, N, K), generator=gen).bfloat16().cuda().requires_grad_()
+    grad = torch.randn((M, N), generator=gen).bfloat16().cuda()
+    cfg = Cfg(format=Format.E4M3, granularity=getattr(SG, gran), block_size=128 if gran == "BLOCKWISE" else None)
+
+    def eager(lens):
+        a.grad = b.grad = None
+        o = turbo.ops.grouped_gemm_fp8(a, b, lens, trans_b=True, config=cfg)
+        o.backward(grad)
+        return o.detach().clone(), a.grad.clone(), b.grad.clone()
+
+    e1, e2 = eager(lens1), eager(lens2)
+    gl = lens1.clone()
+    a.grad = torch.zeros_like(a)
+    b.grad = torch.zeros_like(b)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = turbo.ops.grouped_gemm_fp8(a, b, gl, trans_b=True, config=cfg)
+        out.backward(grad)
+    for lens, exp in ((lens1, e1), (lens2, e2), (lens1, e1), (lens2, e2)):
+        gl.copy_(lens)
+        a.grad.zero_()
+        b.grad.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, exp[0]), "forward"
+        assert torch.equal(a.grad, exp[1]), "dA"
+        assert torch.equal(b.grad, exp[2]), "dB"
+        _ = (a.detach() * 2).sum().item()  # eager work between replays
+    del graph
+    torch.cuda.synchronize()
