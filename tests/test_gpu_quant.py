@@ -428,3 +428,56 @@ def test_reference_mx_roundtrip(orig_dtype, dest_dtype, batched, MN, axis, use_2
     y = turbo.ops.dequantize_fp8(q, orig_dtype, SG.MX_BLOCKWISE, block_size=32, axis=qaxis, scale_inv=s,
                                  scaling_recipe=rec)
     torch.testing.assert_close(_mx_padded_ref(x, qaxis), y, rtol=0.1, atol=0.1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("qdt", FP8)
+@pytest.mark.parametrize("shape,spike_pos", [((1, 100), -1), ((1, 8193), -1), ((512, 3072), 8300), ((512, 3072), -1),
+                                             ((1024, 4096), -1)])
+def test_tensorwise_spike_amax(dtype, qdt, shape, spike_pos):
+    """The reference's partial-tile amax regression case (test_quantization.py:
+    66-95): one spike of 100 in a field of 0.5 sets the scale, bit for bit
+    against the oracle."""
+    turbo, SG, _ = _turbo()
+    x = torch.full(shape, 0.5, dtype=dtype)
+    x.view(-1)[spike_pos] = 100.0
+    q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.TENSORWISE)
+    qo, so = O.quant_tensorwise(x, FMT[qdt])
+    assert_f32_bitexact(f32(s), so, "scale_inv")
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+
+
+@pytest.mark.parametrize("dest_dtype", FP8)
+@pytest.mark.parametrize("BMN", [(1, 32, 256), (4, 64, 32), (4, 256, 1024)])
+@pytest.mark.parametrize("use_2d_block", [True, False])
+def test_reference_mx_with_trans_roundtrip(dest_dtype, BMN, use_2d_block):
+    """The reference's dual MXFP8 criterion (test_quantization.py:369-460): the
+    rowwise copy dequantizes to [M, N_pad], the transposed copy (axis 0) to
+    [M_pad, N], both equal to the zero-padded input at rtol = atol = 0.1 --
+    except where the OCP rule saturates a block maximum to +-fp8_max, which is
+    checked to be exactly that.  (On this seed's 1024 x 1024 input with 32 x 32
+    blocks, 12 such elements are off by more than the reference's tolerance;
+    its own kernel is absent from the snapshot, so whether it saturates the
+    same way is not known.)"""
+    turbo, SG, SR = _turbo()
+    B, M, N = BMN
+    torch.manual_seed(42)
+    x = torch.randn((B * M, N), device="cuda", dtype=torch.bfloat16)
+    rec = SR(use_2d_block=use_2d_block)
+    qr, sr, qt, st = turbo.ops.quantize_fp8_with_trans(x, dest_dtype, SG.MX_BLOCKWISE, block_size=32,
+                                                       scaling_recipe=rec, scaling_recipe_for_trans=rec)
+    yr = turbo.ops.dequantize_fp8(qr, torch.bfloat16, SG.MX_BLOCKWISE, block_size=32, axis=1, scale_inv=sr,
+                                  scaling_recipe=rec)
+    yc = turbo.ops.dequantize_fp8(qt, torch.bfloat16, SG.MX_BLOCKWISE, block_size=32, axis=0, scale_inv=st,
+                                  scaling_recipe=rec)
+    fmax = 448.0 if dest_dtype == torch.float8_e4m3fn else 57344.0
+    for ref, y, sc, transposed in ((_mx_padded_ref(x, 1), yr, sr, False), (_mx_padded_ref(x, 0), yc, st, True)):
+        # per-element block scale 2^(e - 127), in y's layout
+        scale = torch.exp2(sc.view(torch.uint8).float() - 127.0).repeat_interleave(32, dim=-1)
+        scale = scale.t() if transposed else scale
+        ref = ref.float()
+        # OCP MX v1.0: E = floor(log2 amax) - emax, so a block maximum in
+        # [2^emax * 448/256, 2^(emax+1)) saturates to +-fp8_max (error < 12.5%)
+        sat = ref.abs() / scale > fmax
+        torch.testing.assert_close(ref[~sat], y.float()[~sat], rtol=0.1, atol=0.1)
+        assert torch.equal(y.float()[sat], (torch.sign(ref) * fmax * scale)[sat].to(y.dtype).float())
