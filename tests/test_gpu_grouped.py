@@ -400,3 +400,31 @@ def test_grouped_layer_graph_replay(gran):
         _ = (a.detach() * 2).sum().item()  # eager work between replays
     del graph
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
+def test_grouped_deterministic(gran):
+    """Two identical calls give identical bits, forward and both gradients (the
+    reference's *_deterministic tests, test_grouped_gemm_fp8.py:315-435): no
+    atomics or split reductions anywhere on the path."""
+    (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
+    g = getattr(SG, gran)
+    if gran == "MX_BLOCKWISE":
+        from primus_turbo.pytorch.core.low_precision import ScaleDtype
+
+        cfg = Cfg(granularity=g, format=Format.E4M3, block_size=32, scale_dtype=ScaleDtype.E8M0)
+    else:
+        cfg = Cfg(granularity=g, format=Format.E4M3, block_size=128 if gran == "BLOCKWISE" else None)
+    lens = torch.tensor([700, 0, 1300, 96, 2000], dtype=torch.int64, device="cuda")
+    gen = torch.Generator().manual_seed(9)
+    a = torch.randn((int(lens.sum()), 1024), generator=gen).bfloat16().cuda().requires_grad_()
+    b = torch.randn((5, 768, 1024), generator=gen).bfloat16().cuda().requires_grad_()
+    grad = torch.randn((int(lens.sum()), 768), generator=gen).bfloat16().cuda()
+    res = []
+    for _ in range(2):
+        a.grad = b.grad = None
+        o = turbo.ops.grouped_gemm_fp8(a, b, lens, trans_b=True, config=cfg)
+        o.backward(grad)
+        res.append((o.detach().clone(), a.grad.clone(), b.grad.clone()))
+    for x, y in zip(*res):
+        assert torch.equal(x, y)
