@@ -64,3 +64,23 @@ def test_workspace_queries():
     assert _C.query("pta_gemm_fp8_workspace_size", 128, 256, 512, 1, 0, 3) >= 128 * 512 + 256 * 512
     assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 4, 100, 1) == 0
     assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 1, 100, 64) > 0
+
+
+def test_argument_errors_of_the_grouped_and_moe_entries():
+    """Host-side argument checks of the newer entry points fire before any HIP
+    call, with a message naming the problem (so no GPU is needed)."""
+    from primus_turbo.pytorch import _C
+
+    p = ctypes.c_void_p(256)  # never dereferenced: the checks reject first
+    with pytest.raises(RuntimeError, match="unknown layout 7"):
+        _C.call("pta_quantize_fp8_blockwise_segment_m_row_col", p, _C.PTA_BF16, 128, 128, 1, p, p, 128, p, p, p, p,
+                p, p, _C.PTA_E4M3, 7, None)
+    with pytest.raises(RuntimeError, match="MX_BLOCKWISE and BLOCKWISE"):
+        _C.call("pta_grouped_gemm_fp8_variable_k_nt", p, 0, p, p, 0, p, p, 1, 128, 128, 128, p, _C.PTA_BF16, 0,
+                _C.PTA_TENSORWISE, None)
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        _C.call("pta_grouped_gemm_fp8_variable_k_nt", p, 0, p, p, 0, p, p, 1, 192, 128, 128, p, _C.PTA_BF16, 0,
+                _C.PTA_BLOCKWISE, None)
+    with pytest.raises(RuntimeError, match="num_local_experts"):
+        _C.call("pta_moe_permute_preprocess", p, _C.MOE_MAP_BOOL, 16, 600, 0, 0, 16, 0, p, p, p, p, p, 1 << 20,
+                None)
