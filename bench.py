@@ -90,24 +90,30 @@ def _traffic_from_profiles(name: str):
     return None
 
 
-def _cpu_baseline(M, N, K, seed_inputs, budget_s=12.0, max_reps=15):
+def _cpu_baseline(M, N, K, seed_inputs, gpu_out=None, budget_s=12.0, max_reps=15):
     """The CPU oracle's blockwise GEMM (dequantize both operands, fp64 BLAS
     product) over the whole [M x K] x [N x K]^T problem, repeated until about
-    `budget_s` seconds of CPU work; reports the median repetition."""
+    `budget_s` seconds of CPU work; reports the median repetition.  As the
+    checker, its product also gives the GPU output's SNR and max relative
+    error (the stated tolerance: SNR >= 40 dB, max rel <= 1e-2)."""
     from oracle import oracle as O
 
     a_q, a_s, w_q, w_s = seed_inputs
-    times, parts = [], None
+    times, parts, acc = [], None, None
     while len(times) < max_reps and (sum(times) < budget_s or len(times) < 1):
         t0 = time.perf_counter()
         da = O.dequant_block1d(a_q, 0, a_s, 1)
         dw = O.dequant_block2d(w_q, 0, w_s)
         t1 = time.perf_counter()
-        _ = O.gemm_ref(da, dw, False, True)
+        ref = O.gemm_ref(da, dw, False, True)
         t2 = time.perf_counter()
         times.append(t2 - t0)
         parts = (t1 - t0, t2 - t1)
-        del da, dw, _
+        if acc is None and gpu_out is not None:
+            acc = {"snr_db": round(O.snr_db(ref, gpu_out), 2), "max_rel_err": float(f"{O.max_rel_err(ref, gpu_out):.3e}"),
+                   "tolerance": "SNR >= 40 dB and max rel <= 1e-2",
+                   "reference": "fp64 product of the dequantized FP8 operands (CPU oracle), whole output"}
+        del da, dw, ref
     times.sort()
     med = times[len(times) // 2]
     flops = 2.0 * M * N * K
@@ -124,7 +130,7 @@ def _cpu_baseline(M, N, K, seed_inputs, budget_s=12.0, max_reps=15):
         "kind": "port",
         "sample": f"whole {M}x{N}x{K} GEMM, median of {len(times)}: dequantize ({parts[0]:.2f} s) + fp64 BLAS "
                   f"matmul ({parts[1]:.2f} s) in oracle/oracle.py",
-    }
+    }, acc
 
 
 def main():
@@ -191,12 +197,13 @@ def main():
         del grad
         extras["other_configs"] = _other_configs(args)
 
-    cpu = None
+    cpu, accuracy = None, None
     if not args.no_cpu_baseline:
-        cpu = _cpu_baseline(
+        cpu, accuracy = _cpu_baseline(
             M, N, K,
             (a_row.cpu().view(torch.uint8).numpy(), a_s.cpu().numpy(),
              w_q.cpu().view(torch.uint8).numpy(), w_s.cpu().numpy()),
+            gpu_out=out.float().cpu().numpy(),
         )
 
     if args.copy_calibration:
@@ -233,6 +240,7 @@ def main():
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
+        "accuracy": accuracy,
     }
     line.update(extras)
     print(json.dumps(line))
