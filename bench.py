@@ -199,12 +199,13 @@ def main():
 
     cpu, accuracy = None, None
     if not args.no_cpu_baseline:
-        cpu, accuracy = _cpu_baseline(
-            M, N, K,
-            (a_row.cpu().view(torch.uint8).numpy(), a_s.cpu().numpy(),
-             w_q.cpu().view(torch.uint8).numpy(), w_s.cpu().numpy()),
-            gpu_out=out.float().cpu().numpy(),
-        )
+        import numpy as np
+
+        host = (a_row.cpu().view(torch.uint8).numpy(), a_s.cpu().numpy(),
+                w_q.cpu().view(torch.uint8).numpy(), w_s.cpu().numpy())
+        cpu, accuracy = _cpu_baseline(M, N, K, host, gpu_out=out.float().cpu().numpy())
+        accuracy["quantize_bitexact"] = _quant_parity(a.cpu(), w.cpu(), host[0], np.ascontiguousarray(host[1]),
+                                                      host[2], host[3])
 
     if args.copy_calibration:
         x = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
@@ -244,6 +245,22 @@ def main():
     }
     line.update(extras)
     print(json.dumps(line))
+
+
+def _quant_parity(a_cpu, w_cpu, a_q, a_s, w_q, w_s):
+    """Checker run with the CPU baseline: the timed quantizers' FP8 bytes and
+    scales against the CPU oracle's, element for element (the bar is bit-exact)."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    qr, sr, _, _ = O.quant_block_dual(a_cpu, 0)
+    qw, sw = O.quant_block_weight(w_cpu, 0)
+    return {
+        "activation_1x128": bool(np.array_equal(qr, a_q) and np.array_equal(sr.view(np.uint32), a_s.view(np.uint32))),
+        "weight_128x128": bool(np.array_equal(qw, w_q) and np.array_equal(sw.view(np.uint32), w_s.view(np.uint32))),
+        "reference": "CPU oracle (oracle/fp8_oracle.c), bytes and fp32 scale bits",
+    }
 
 
 def _gemm_rec(ms, flops):
