@@ -481,3 +481,19 @@ def test_reference_mx_with_trans_roundtrip(dest_dtype, BMN, use_2d_block):
         sat = ref.abs() / scale > fmax
         torch.testing.assert_close(ref[~sat], y.float()[~sat], rtol=0.1, atol=0.1)
         assert torch.equal(y.float()[sat], (torch.sign(ref) * fmax * scale)[sat].to(y.dtype).float())
+
+
+@pytest.mark.parametrize("BMN", [(4, 111, 1), (1, 1, 4096), (4, 7168, 111), (1, 111, 4096)])
+@pytest.mark.parametrize("axis", [-1, -2, -3, 0, 1, 2])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_rowwise_reference_axes_vs_oracle(BMN, axis, dtype):
+    """The reference's rowwise parametrization (test_quantization.py:98-140:
+    every axis of a [B, M, N] input, sizes 1 / 111 / 4096 / 7168), held to
+    bit-exact bytes and scales against the oracle instead of a tolerance."""
+    turbo, SG, _ = _turbo()
+    x = _input(BMN, dtype, seed=12, special=False)
+    q, s = turbo.ops.quantize_fp8(x.cuda(), torch.float8_e4m3fn, SG.ROWWISE, axis=axis)
+    qo, so = O.quant_rowwise(x, FMT[torch.float8_e4m3fn], axis)
+    assert tuple(s.shape) == so.shape
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+    assert_f32_bitexact(f32(s), so, "scale_inv")
