@@ -333,3 +333,14 @@ def test_reference_float8linear_criterion(gran, dtype, fmt, bias):
         assert s > 20, f"{name} SNR {s:.1f} dB"
     if bias:
         torch.testing.assert_close(lin.bias.grad, bg_ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("m", [176, 512])
+@pytest.mark.parametrize("n", [256, 352])
+@pytest.mark.parametrize("k", [128, 160])
+@pytest.mark.parametrize("fmt", ["E4M3", "E5M2", "HYBRID"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_fp8_mx_reference_grid(m, n, k, fmt, dtype):
+    """The reference's MX gemm_fp8 grid (test_gemm_fp8.py:293-330: ragged m/n,
+    k = 128 / 160, all three formats, bf16 and fp16 outputs), its SNR criterion."""
+    _autograd_case(m, n, k, "NT", fmt, "MX_BLOCKWISE", block_size=32, dtype=dtype)
