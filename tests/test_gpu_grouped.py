@@ -474,3 +474,55 @@ def test_grouped_gemm_fp8_quantized_tensor_inputs(gran, trans_b):
     for name, x, r in (("out", out, ref), ("dA", qa.grad, a_ref.grad), ("dB", qb.grad, b_ref.grad)):
         s = O.snr_db(f32(r), f32(x))
         assert s > 25, f"{name} SNR {s:.1f} dB"
+
+
+def _ref_group_lens(b, m, seed):
+    """Unbalanced split as the reference's generator draws it (tests/pytorch/ref/
+    gemm_ref.py:77-86): weights 0.2 + 0.8 U(0,1), normalised to b*m rows."""
+    gen = torch.Generator().manual_seed(seed)
+    dist = 0.2 + 0.8 * torch.rand(b, generator=gen)
+    dist /= dist.sum()
+    lens = (dist * b * m).to(torch.int64)
+    lens[-1] += b * m - lens.sum()
+    return lens
+
+
+@pytest.mark.parametrize("B,M", [(1, 256), (3, 512), (8, 128), (16, 256)])
+@pytest.mark.parametrize("NK", [(2048, 1408), (1408, 2048)])
+@pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
+@pytest.mark.parametrize("fmt", ["E4M3", "E5M2"])
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_grouped_reference_grid(B, M, NK, gran, fmt, trans_b):
+    """A slice of the reference's grouped grid (test_grouped_gemm_fp8.py:35-50,
+    437-570: its B / M / (N, K) values, unbalanced splits, both formats and
+    weight layouts) at its SNR criterion: > 25 dB for e4m3, > 20 for e5m2."""
+    (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
+    g = getattr(SG, gran)
+    if g == SG.MX_BLOCKWISE and not trans_b:
+        pytest.skip("MXFP8 grouped GEMM is NT only, as in the reference (grouped_gemm_fp8.py:603)")
+    N, K = NK
+    lens = _ref_group_lens(B, M, seed=B * 1000 + M).cuda()
+    gen = torch.Generator().manual_seed(B + M)
+    a = torch.randn((B * M, K), generator=gen).bfloat16().cuda().requires_grad_()
+    b = torch.randn((B, N, K) if trans_b else (B, K, N), generator=gen).bfloat16().cuda().requires_grad_()
+    if g == SG.MX_BLOCKWISE:
+        from primus_turbo.pytorch.core.low_precision import ScaleDtype
+
+        cfg = Cfg(granularity=g, format=getattr(Format, fmt), block_size=32, scale_dtype=ScaleDtype.E8M0)
+    else:
+        cfg = Cfg(granularity=g, format=getattr(Format, fmt), block_size=128 if gran == "BLOCKWISE" else None)
+    out = turbo.ops.grouped_gemm_fp8(a, b, lens, trans_b=trans_b, config=cfg)
+    grad = torch.randn(out.shape, generator=gen).bfloat16().cuda()
+    out.backward(grad)
+    a_ref = a.detach().float().requires_grad_()
+    b_ref = b.detach().float().requires_grad_()
+    outs, off = [], 0
+    for i, L in enumerate(lens.tolist()):
+        outs.append(a_ref[off:off + L] @ (b_ref[i].T if trans_b else b_ref[i]))
+        off += L
+    ref = torch.cat(outs)
+    ref.backward(grad.float())
+    thr = 25 if fmt == "E4M3" else 20
+    for name, x, r in (("out", out, ref), ("dA", a.grad, a_ref.grad), ("dB", b.grad, b_ref.grad)):
+        s = O.snr_db(f32(r), f32(x))
+        assert s > thr, f"{name} SNR {s:.1f} dB"
