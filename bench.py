@@ -14,9 +14,11 @@ of gemm_fp8 (quantize + NT fwd + dgrad + wgrad), reported as extra fields.
 Roofline: the dominant kernel is the GEMM (MFMA-bound); peak = 5.0 PFLOP/s
 dense FP8 (MI355X).  The quantize kernels are HBM-bound, peak 8 TB/s.
 
-cpu_baseline: the CPU oracle (oracle/oracle.py: dequantize both operands,
-fp64 BLAS product) on the same GEMM, repeated up to ~10 s of CPU work, median
-reported in TFLOP/s with the BLAS thread count.
+cpu_baseline: the reference's torch CPU path for the same GEMM restated with
+torch CPU ops (blockwise quantize, dequantize, fp32 matmul, bf16 out), repeated
+for about 15 s of CPU work, median reported in TFLOP/s with torch's thread
+count (os.cpu_count() reported beside it).  The timed GPU output is checked
+separately against the CPU oracle's fp64 product (the `accuracy` field).
 
 Profiling: --only gemm times the headline GEMM alone and --copy-calibration
 appends three 256 MiB device copies, whose FETCH_SIZE / WRITE_SIZE readings
@@ -57,22 +59,9 @@ def _time_cuda(fn, steps: int, warmup: int):
 
 
 def _time_settled(fn, steps: int, settle_ms: float = 40.0):
-    """_time_cuda after running fn until settle_ms of GPU time has passed: the
-    clock ramps down while the host prepares a configuration's inputs, and a
-    few warm-up calls do not bring it back."""
-    import torch
-
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    n, spent = 0, 0.0
-    while spent < settle_ms and n < 10000:
-        start.record()
-        for _ in range(4):
-            fn()
-        end.record()
-        torch.cuda.synchronize()
-        spent += start.elapsed_time(end)
-        n += 4
+    """_time_cuda after _settle: each extra measurement first runs its call
+    until settle_ms of GPU time has passed."""
+    _settle(fn, settle_ms)
     return _time_cuda(fn, steps, 0)
 
 
@@ -90,55 +79,101 @@ def _traffic_from_profiles(name: str):
     return None
 
 
-def _cpu_baseline(M, N, K, seed_inputs, gpu_out=None, budget_s=12.0, max_reps=15):
-    """The CPU oracle's blockwise GEMM (dequantize both operands, fp64 BLAS
-    product) over the whole [M x K] x [N x K]^T problem, repeated until about
-    `budget_s` seconds of CPU work; reports the median repetition.  As the
-    checker, its product also gives the GPU output's SNR and max relative
-    error (the stated tolerance: SNR >= 40 dB, max rel <= 1e-2)."""
+def _settle(fn, settle_ms: float = 40.0) -> float:
+    """Run fn until settle_ms of GPU time has passed (untimed): the clock ramps
+    down while the host prepares inputs and takes tens of milliseconds of
+    load to come back.  Returns the GPU milliseconds spent."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    n, spent = 0, 0.0
+    while spent < settle_ms and n < 10000:
+        start.record()
+        for _ in range(4):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        spent += start.elapsed_time(end)
+        n += 4
+    return spent
+
+
+def _cpu_baseline(a_cpu, w_cpu, budget_s=15.0, max_reps=9):
+    """The reference's torch CPU path for this GEMM, restated with torch CPU
+    ops: blockwise quantization as the reference's torch quantize ref does it
+    in fp32 (tests/pytorch/ref/quantization_ref.py; 1x128 activation and
+    128x128 weight blocks, eps 1e-4, scale = fp8_max / amax, clamp, e4m3
+    cast), dequantization, an fp32 matmul (tests/pytorch/ref/gemm_ref.py:13-24
+    accumulates in fp32) and the bf16 output.  One warm-up, then repetitions
+    until about `budget_s` seconds; the median is reported.  Threads: torch's
+    intra-op pool as the box sets it (its CPU share), reported beside
+    os.cpu_count()."""
+    import torch
+
+    M, K = a_cpu.shape
+    N = w_cpu.shape[0]
+    fmax = 448.0
+
+    def q_act(x):
+        xf = x.float().view(M, K // 128, 128)
+        s = fmax / torch.clamp(xf.abs().amax(-1, keepdim=True), min=1e-4)
+        return torch.clamp(xf * s, -fmax, fmax).to(torch.float8_e4m3fn), 1.0 / s
+
+    def q_w(x):
+        xf = x.float().view(N // 128, 128, K // 128, 128)
+        s = fmax / torch.clamp(xf.abs().amax(dim=(1, 3), keepdim=True), min=1e-4)
+        return torch.clamp(xf * s, -fmax, fmax).to(torch.float8_e4m3fn), 1.0 / s
+
+    def step():
+        qa, sa = q_act(a_cpu)
+        qw, sw = q_w(w_cpu)
+        da = (qa.float() * sa).view(M, K)
+        dw = (qw.float() * sw).view(N, K)
+        return (da @ dw.t()).to(torch.bfloat16)
+
+    step()
+    times = []
+    while len(times) < max_reps and (sum(times) < budget_s or len(times) < 3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    threads = torch.get_num_threads()
+    print(f"cpu_baseline: os.cpu_count()={os.cpu_count()} torch.get_num_threads()={threads}", file=sys.stderr)
+    return {
+        "value": 2.0 * M * N * K / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "os_cpu_count": os.cpu_count(),
+        "torch_threads": int(threads),
+        "sample": f"whole {M}x{N}x{K} blockwise step on the CPU (torch fp32: quantize A 1x128 and W 128x128, "
+                  f"dequantize, matmul, bf16), median of {len(times)} after 1 warm-up",
+    }
+
+
+def _accuracy(seed_inputs, gpu_out):
+    """Checker of the timed output: the CPU oracle's fp64 product of the same
+    dequantized FP8 operands over the whole output (the stated tolerance:
+    SNR >= 40 dB, max rel <= 1e-2)."""
     from oracle import oracle as O
 
     a_q, a_s, w_q, w_s = seed_inputs
-    times, parts, acc = [], None, None
-    while len(times) < max_reps and (sum(times) < budget_s or len(times) < 1):
-        t0 = time.perf_counter()
-        da = O.dequant_block1d(a_q, 0, a_s, 1)
-        dw = O.dequant_block2d(w_q, 0, w_s)
-        t1 = time.perf_counter()
-        ref = O.gemm_ref(da, dw, False, True)
-        t2 = time.perf_counter()
-        times.append(t2 - t0)
-        parts = (t1 - t0, t2 - t1)
-        if acc is None and gpu_out is not None:
-            acc = {"snr_db": round(O.snr_db(ref, gpu_out), 2), "max_rel_err": float(f"{O.max_rel_err(ref, gpu_out):.3e}"),
-                   "tolerance": "SNR >= 40 dB and max rel <= 1e-2",
-                   "reference": "fp64 product of the dequantized FP8 operands (CPU oracle), whole output"}
-        del da, dw, ref
-    times.sort()
-    med = times[len(times) // 2]
-    flops = 2.0 * M * N * K
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    return {
-        "value": flops / med / 1e12,
-        "unit": "TFLOP/s",
-        "cores": int(cores),
-        "kind": "port",
-        "sample": f"whole {M}x{N}x{K} GEMM, median of {len(times)}: dequantize ({parts[0]:.2f} s) + fp64 BLAS "
-                  f"matmul ({parts[1]:.2f} s) in oracle/oracle.py",
-    }, acc
+    ref = O.gemm_ref(O.dequant_block1d(a_q, 0, a_s, 1), O.dequant_block2d(w_q, 0, w_s), False, True)
+    return {"snr_db": round(O.snr_db(ref, gpu_out), 2), "max_rel_err": float(f"{O.max_rel_err(ref, gpu_out):.3e}"),
+            "tolerance": "SNR >= 40 dB and max rel <= 1e-2",
+            "reference": "fp64 product of the dequantized FP8 operands (CPU oracle), whole output"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=100,
-                    help="untimed calls before the timed ones (~50 ms: the clock settles after input setup)")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed calls after the settle, before the timed ones")
+    ap.add_argument("--settle-ms", type=float, default=60.0,
+                    help="GPU milliseconds of untimed calls before the warm-up (the clock settles after input setup)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "gemm"], default="all",
                     help="gemm: time only the headline GEMM (for counter passes)")
@@ -187,6 +222,9 @@ def main():
     def gemm():
         gemm_fp8_nt(a_row, w_q, torch.bfloat16, SG.BLOCKWISE, a_s, a_s.stride(), False, w_s, (nbk, 1), True, out=out)
 
+    # settle the clock by time first (the count-based warm-up alone is too
+    # short for a 0.5 ms kernel), then the W warm-up calls, then K timed ones
+    settle_ms = _settle(gemm, args.settle_ms)
     ms = _time_cuda(gemm, args.steps, args.warmup)
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
@@ -203,9 +241,10 @@ def main():
 
         host = (a_row.cpu().view(torch.uint8).numpy(), a_s.cpu().numpy(),
                 w_q.cpu().view(torch.uint8).numpy(), w_s.cpu().numpy())
-        cpu, accuracy = _cpu_baseline(M, N, K, host, gpu_out=out.float().cpu().numpy())
+        accuracy = _accuracy(host, out.float().cpu().numpy())
         accuracy["quantize_bitexact"] = _quant_parity(a.cpu(), w.cpu(), host[0], np.ascontiguousarray(host[1]),
                                                       host[2], host[3])
+        cpu = _cpu_baseline(a.cpu(), w.cpu())
 
     if args.copy_calibration:
         x = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
@@ -223,6 +262,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "settle_ms": round(settle_ms, 1),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

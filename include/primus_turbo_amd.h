@@ -399,8 +399,8 @@ int pta_moe_permute(const void *tokens, int64_t num_tokens, int elem_bytes, int6
  * positive slots d); with one expert and a probs width of 1 the single row is
  * copied bit for bit.  dtype is PTA_BF16 or PTA_F16, hidden % 8 == 0.
  * probs[t, :] (width probs_stride or E) = permuted_probs[d - 1] at the aux
- * column of each positive slot, 0 elsewhere.  Rows t >= *num_dispatched are
- * not written.
+ * column of each positive slot, 0 elsewhere.  Rows *num_dispatched <= t <
+ * num_tokens are written as zeros (tokens and probs).
  * Replaces unpermute (csrc/pytorch/moe_permute/moe_permute.cpp:214-276,
  * kernels csrc/kernels/moe_permute/moe_permute.cu:507-602). */
 int pta_moe_unpermute(const void *permuted, int64_t num_permuted, int dtype, int64_t hidden,

@@ -309,12 +309,18 @@ OR_EXPORT void or_quant_block_segment(const void *x, int in_dt, int64_t M, int64
 /* ------------------------------------------------------------------------- */
 /* MXFP8 (block 32, E8M0 shared exponent).                                    */
 /* The reference's quantize kernel source is absent from the snapshot; the   */
-/* surviving constants (csrc/include/primus_turbo/quantization.h:88-102:      */
-/* FP8E4M3_TARGET_MAX_POW2 = 8, FP8E5M2_TARGET_MAX_POW2 = 15,                 */
-/* E8M0_EXPONENT_BIAS = 127) encode the OCP MX v1.0 rule restated here:       */
-/*   E     = floor(log2(amax)) - emax_elem                                    */
+/* surviving constants (csrc/include/primus_turbo/quantization.h:85-102:      */
+/* FP8E4M3_TARGET_MAX_POW2 = 8, FP8E5M2_TARGET_MAX_POW2 = 15, the mantissa    */
+/* widths and E8M0_EXPONENT_BIAS = 127) and the reference's own round-trip   */
+/* test (tests/pytorch/ops/test_quantization.py:304-460, rtol = atol = 0.1    */
+/* against the dequantized value) fix the rule restated here:                 */
+/*   E     = floor(log2(amax)) - emax_elem,                                   */
+/*           plus 1 when amax * 2^-E > fp8_max (the block maximum would       */
+/*           otherwise saturate: mantissa of amax above 1.75)                 */
 /*   e8m0  = clamp(E + 127, 0, 254)        (amax == 0 -> 0)                   */
 /*   q     = cast(clamp(x * 2^(127 - e8m0), +-max))                           */
+/* The plain OCP floor rule (no bump) saturates every block whose amax       */
+/* mantissa exceeds 1.75 and fails that test at its 1024 x 1024 sizes.       */
 /* decode: scale = bits(e8m0 << 23) (csrc/include/primus_turbo/device/        */
 /* utils.cuh:117-120), so e8m0 == 0 decodes to 0.0.                           */
 /* Layouts (quantization.cpp:736-858): row q[G*M, N_pad] s[G*M, N_pad/32];    */
@@ -322,11 +328,15 @@ OR_EXPORT void or_quant_block_segment(const void *x, int in_dt, int64_t M, int64
 /* elements are 0.  use_2d_block shares one exponent per 32 x 32 tile.        */
 /* ------------------------------------------------------------------------- */
 static inline int mx_e8m0_of(float amax, int fmt) {
-    const int emax = fmt == 0 ? 8 : 15;
+    const int   emax = fmt == 0 ? 8 : 15;
+    const float fmax = fmt == 0 ? 448.0f : 57344.0f;
     if (!(amax > 0.0f)) return 0;
+    if (isinf(amax)) return 255 - emax; /* biased exponent field 255, no bump */
     int e2;
-    frexpf(amax, &e2);
-    int e = (e2 - 1) - emax + 127;
+    frexpf(amax, &e2);                 /* amax = f * 2^e2, f in [0.5, 1) */
+    int E = (e2 - 1) - emax;           /* floor(log2 amax) - emax */
+    if (ldexpf(amax, -E) > fmax) E += 1; /* exact: a power-of-two scaling */
+    int e = E + 127;
     if (e < 0) e = 0;
     if (e > 254) e = 254;
     return e;

@@ -1,4 +1,5 @@
-// Driver for the reference's own HIP quantization and MoE permutation kernels --
+// Driver for the reference's own HIP quantization, MX dequantization, transpose
+// and MoE permutation kernels --
 // TEST INFRASTRUCTURE ONLY.
 //
 // oracle/Makefile.ref compiles this file together with the reference's kernel
@@ -17,6 +18,7 @@
 #include "primus_turbo/quantization.h"
 #include "primus_turbo/reduce.h"
 #include "primus_turbo/shuffle.h"
+#include "primus_turbo/transpose.h"
 
 using namespace primus_turbo;
 using bf16 = dtype::bfloat16;
@@ -185,6 +187,35 @@ int ref_moe_unpermute(const void *perm, void *out, int is_bf16, const float *ppr
         unpermute_impl<dtype::float16, float>(reinterpret_cast<const dtype::float16 *>(perm),
                                               reinterpret_cast<dtype::float16 *>(out), pprobs, oprobs, row_id_map,
                                               ndisp, E, H, T, probs_stride, st);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// MX dequantize of a 2-D q[rows, cols] with E8M0 e[e_rows, e_cols] (row-major),
+// replaying dequantize_mxfp8 (csrc/pytorch/quantization/quantization.cpp:283-357):
+// rowwise writes y[rows, cols]; colwise (axis 0) writes the transpose
+// y[cols, rows].  out_dt 0 = fp32, 2 = bf16 (the C ABI's type codes).
+int ref_dequant_mxfp8(const void *q, int fmt, int64_t rows, int64_t cols, const uint8_t *e, int64_t e_rows,
+                      int64_t e_cols, int rowwise, void *y, int out_dt, void *stream) {
+    hipStream_t   st  = reinterpret_cast<hipStream_t>(stream);
+    const int64_t ys0 = rowwise ? cols : rows; // output_2d.stride(0)
+#define PTA_REF_DQ(OT, QT)                                                                                    \
+    dequantize_mxfp8_impl<OT, QT>(reinterpret_cast<const QT *>(q), reinterpret_cast<OT *>(y), cols, 1, ys0, 1, \
+                                  static_cast<int>(rows), static_cast<int>(cols), e, e_cols, 1,               \
+                                  static_cast<int>(e_rows), static_cast<int>(e_cols), 32, rowwise != 0, st)
+    if (out_dt == 2) {
+        if (fmt == 0) PTA_REF_DQ(dtype::bfloat16, dtype::float8_e4m3);
+        else PTA_REF_DQ(dtype::bfloat16, dtype::float8_e5m2);
+    } else {
+        if (fmt == 0) PTA_REF_DQ(dtype::float32, dtype::float8_e4m3);
+        else PTA_REF_DQ(dtype::float32, dtype::float8_e5m2);
+    }
+#undef PTA_REF_DQ
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// transpose_2d (csrc/pytorch/transpose/transpose.cpp): x[batch, M, N] -> y[batch, N, M]
+int ref_transpose_2d(const void *x, void *y, int64_t batch, int64_t M, int64_t N, int64_t itemsize, void *stream) {
+    transpose_2d_impl(x, y, batch, M, N, itemsize, reinterpret_cast<hipStream_t>(stream));
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 

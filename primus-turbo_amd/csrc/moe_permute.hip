@@ -373,7 +373,9 @@ __device__ __forceinline__ mp_v4u round8(const float (&a)[8]) {
 }
 
 // Token t < nd: out[t] = round(sum over the row's positive slots, in row
-// order, of fp32(permuted[slot - 1])), starting from +0.0.  copy_rows (one
+// order, of fp32(permuted[slot - 1])), starting from +0.0; tokens
+// nd <= t < T get zero rows (and zero probs), so no output row is left
+// unwritten when fewer tokens were dispatched than restored.  copy_rows (one
 // expert, probs width 1) copies the single source row bit for bit instead, as
 // the reference's unpermute_kernel_e1 does.  Row layout over threads as in
 // mp_permute_kernel; sources are read MP_GRP rows at a time.
@@ -402,7 +404,7 @@ __global__ __launch_bounds__(256) void mp_unpermute_kernel(const uint8_t *perm, 
         aux[j]      = row[E + j];
     }
     __syncthreads();
-    if (!active) return;
+    if (tok >= T) return; // inactive tokens below T fall through with n = 0: zero rows
 
     const int64_t rb     = H * 2;
     const int64_t nchunk = rb >> 4;
@@ -572,7 +574,9 @@ extern "C" int pta_moe_unpermute(const void *permuted, int64_t num_permuted, int
     PTA_CHECK_ARG(hidden >= 0 && num_tokens >= 0 && num_permuted >= 0, "negative size");
     PTA_CHECK_ARG(hidden % 8 == 0, "unpermute: hidden_size must be a multiple of 8");
     PTA_CHECK_ARG(probs_stride >= 0, "probs_stride must be >= 0");
-    PTA_CHECK_ARG((permuted_probs == nullptr) == (probs == nullptr), "permuted_probs and probs go together");
+    // an empty permuted operand may come with a NULL probs pointer (no row to read)
+    PTA_CHECK_ARG(permuted_probs == nullptr ? (probs == nullptr || num_permuted == 0) : probs != nullptr,
+                  "permuted_probs and probs go together");
     if (num_tokens == 0) return PTA_OK;
     PTA_CHECK_ARG(tokens && row_id_map && num_dispatched && (permuted || num_permuted == 0), "null pointer");
     PTA_CHECK_ARG(aligned16(tokens) && (permuted == nullptr || aligned16(permuted)),

@@ -241,11 +241,16 @@ __global__ __launch_bounds__(NT) void rw_col_quant_kernel(const void *x, int64_t
 // Rowwise: lane t owns row t>>2 ... using 4 lanes per 64-col row, 16 cols each.
 // Colwise: the tile is staged in LDS and lane t owns column t>>2, 16 rows.
 // ---------------------------------------------------------------------------
+// Shared exponent of a block: E = floor(log2 amax) - emax, plus 1 when the
+// block maximum would saturate (amax * 2^-E > fp8_max).  Both fp8 maxima are
+// 1.75 * 2^emax, so for a normal amax the bump is "mantissa above 1.75"; a
+// subnormal amax clamps to 0 either way.  Biased: e8m0 = clamp(E + 127, 0, 254).
 template <int FMT> __device__ __forceinline__ int mx_e8m0(float amax) {
-    constexpr int emax = FMT == PTA_E4M3 ? 8 : 15;
-    const int     be   = static_cast<int>((__float_as_uint(amax) >> 23) & 0xffu);
-    int           e    = be - emax;
-    e                  = e < 0 ? 0 : (e > 254 ? 254 : e);
+    constexpr int  emax = FMT == PTA_E4M3 ? 8 : 15;
+    const uint32_t bits = __float_as_uint(amax);
+    const int      be   = static_cast<int>((bits >> 23) & 0xffu);
+    int            e    = be - emax + ((be != 0 && (bits & 0x7fffffu) > 0x600000u) ? 1 : 0);
+    e                   = e < 0 ? 0 : (e > 254 ? 254 : e);
     return amax > 0.0f ? e : 0;
 }
 __device__ __forceinline__ float mx_qscale(int e8m0) {

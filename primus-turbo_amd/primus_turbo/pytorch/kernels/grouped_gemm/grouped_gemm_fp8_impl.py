@@ -108,6 +108,14 @@ def grouped_gemm_fp8_variable_k_impl(
         return grouped_gemm_fp8_variable_k_nt_impl(a, b, a_scales, b_scales, group_lens.shape[0], group_offs,
                                                    trans_c, out_dtype, gran)
     assert trans_a and not trans_b, "variable-K grouped GEMM expects trans_a=True, trans_b=False"
+    if gran == ScalingGranularity.BLOCKWISE.value:
+        # a 128-row scale block of a [M_total/128, OUT] column scale must not
+        # straddle two groups: the kernel indexes scale rows by padded segment
+        # offset / 128, which is only the quantizer's row when the offsets are
+        # 128-aligned (the segment quant's vk_offs are).  One host read.
+        if bool(torch.any(group_offs.to(torch.int64) % 128 != 0).item()):
+            raise RuntimeError("variable-K BLOCKWISE grouped GEMM needs 128-aligned group offsets "
+                               "(the segment quant's padded offsets)")
     a = a.contiguous()
     b = b.contiguous()
     M_total, OUT_M = a.shape

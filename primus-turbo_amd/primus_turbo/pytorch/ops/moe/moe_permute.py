@@ -1,15 +1,25 @@
-"""MoE token permute / unpermute with autograd (same API as the reference's
-primus_turbo/pytorch/ops/moe/moe_permute.py:17-420).
+"""MoE token permute / unpermute with autograd.
+
+Public API (``moe_permute`` / ``moe_unpermute``: names, keyword arguments and
+return tuples) follows the reference's primus_turbo/pytorch/ops/moe/
+moe_permute.py:353-420.
 
 ``moe_permute`` packs the dispatched tokens expert-major (each expert's rows
 contiguous, optionally padded per expert to ``pad_multiple`` with zero rows):
 the layout and ``tokens_per_expert`` that ``grouped_gemm_fp8`` consumes as
 ``group_lens``.  ``moe_unpermute`` sums each token's expert rows back (fp32
-accumulation).  Each is the other's backward.
+accumulation, row_id_map order).
+
+Design: a ``_Routing`` record holds everything both directions need (the
+row_id_map, the device-side dispatched count and the layout parameters).  Two
+movers, ``_expert_major`` (scatter) and ``_token_major`` (gather-reduce),
+implement the two directions once; each autograd Function runs one of them
+forward and the other backward.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Optional, Tuple
 
 import torch
@@ -23,116 +33,131 @@ from primus_turbo.pytorch.kernels.moe.moe_permute_impl import (
 __all__ = ["moe_permute", "moe_unpermute"]
 
 
-class _MoEPermute(torch.autograd.Function):
-    """Forward: preprocessing + scatter.  Backward: gather-reduce of the
-    gradient (+ probs gradient) (moe_permute.py:17-218)."""
+@dataclass
+class _Routing:
+    row_id_map: torch.Tensor  # [T + pad_multiple, 2E + 1] int32
+    num_dispatched: torch.Tensor  # [1] int32, device
+    num_experts: int
+    pad_multiple: int
+    probs_stride: int  # > 0: probs rows are top-k aligned with this width; 0: num_experts wide
+
+    @property
+    def probs_width(self) -> int:
+        return self.probs_stride if self.probs_stride > 0 else self.num_experts
+
+
+def _route(expert_map, num_tokens, num_experts, num_topk, pad_multiple, cap, probs_stride, device):
+    """Slot assignment for every (token, local expert) pair.  Returns the
+    routing record plus tokens_per_expert and the overflow flag."""
+    if num_tokens == 0:
+        # nothing to assign: an all-zero map of padding rows only
+        rim = torch.zeros((pad_multiple, 2 * num_experts + 1), dtype=torch.int32, device=device)
+        nd = torch.zeros((1,), dtype=torch.int32, device=device)
+        tpe = torch.zeros((num_experts,), dtype=torch.int64, device=device)
+        ovf = torch.zeros((1,), dtype=torch.int32, device=device)
+    else:
+        rim, tpe, ovf, nd = permute_preprocessing_impl(expert_map, num_experts, num_topk, pad_multiple, cap,
+                                                       probs_stride)
+    return _Routing(rim, nd, num_experts, pad_multiple, probs_stride), tpe, ovf
+
+
+def _expert_major(r: _Routing, src: torch.Tensor, n_rows: int, probs: Optional[torch.Tensor] = None,
+                  scales: Optional[torch.Tensor] = None, scales_per_token: int = 0, fp8: bool = False):
+    """Scatter token rows (and their probs / fp8 scaling factors) into
+    ``n_rows`` expert-major rows; padding rows come out zero."""
+    dev, H = src.device, int(src.shape[-1])
+    rows = torch.empty((n_rows, H), dtype=src.dtype, device=dev)
+    out_probs = torch.empty((n_rows,), dtype=probs.dtype, device=dev) if probs is not None else None
+    out_scales = (torch.empty((n_rows, scales_per_token), dtype=scales.dtype, device=dev)
+                  if scales is not None else None)
+    if n_rows > 0 and src.shape[0] > 0:
+        permute_impl(src.contiguous(), rows, scales, out_scales,
+                     probs.contiguous() if probs is not None else None, out_probs, r.row_id_map,
+                     r.num_dispatched, r.pad_multiple, r.num_experts, H, scales_per_token, fp8,
+                     probs is not None, n_rows, r.probs_stride)
+    return rows, out_probs, out_scales
+
+
+def _token_major(r: _Routing, src: torch.Tensor, n_tokens: int, probs: Optional[torch.Tensor] = None):
+    """Gather-reduce expert-major rows (and per-row probs) back into
+    ``n_tokens`` token rows.  Every token row is written: tokens with no
+    routed row, and rows past the dispatched count, come out zero."""
+    dev, H = src.device, int(src.shape[-1])
+    tokens = torch.empty((n_tokens, H), dtype=src.dtype, device=dev)
+    out_probs = (torch.empty((n_tokens, r.probs_width), dtype=probs.dtype, device=dev)
+                 if probs is not None else None)
+    if n_tokens > 0:
+        unpermute_impl(src.contiguous(), tokens, probs.contiguous() if probs is not None else None, out_probs,
+                       r.row_id_map, r.num_dispatched, r.num_experts, H, probs is not None, r.probs_stride)
+    return tokens, out_probs
+
+
+def _save(ctx, r: _Routing) -> None:
+    ctx.save_for_backward(r.row_id_map, r.num_dispatched)
+    ctx.layout = (r.num_experts, r.pad_multiple, r.probs_stride)
+
+
+def _load(ctx) -> _Routing:
+    rim, nd = ctx.saved_tensors
+    return _Routing(rim, nd, *ctx.layout)
+
+
+class _Permute(torch.autograd.Function):
+    """Forward scatters the tokens expert-major; backward gathers the row
+    gradients (and the probs gradient) back per token."""
 
     @staticmethod
-    def forward(ctx, tokens, expert_map, num_local_experts, num_topk, pad_multiple=0, num_permuted_tokens=-1,
-                scaling_factor=None, probs=None, scales_per_token=0, use_fp8=False, probs_topk_stride=0):
-        dev = tokens.device
-        H = int(tokens.shape[-1])
-        T = int(tokens.shape[0])
-        probs_topk_stride = int(probs_topk_stride) if probs is not None else 0
-        row_width = probs_topk_stride if probs_topk_stride > 0 else num_local_experts
-        ctx.num_dispatched, ctx.hidden_size, ctx.num_local_experts = T, H, num_local_experts
-        ctx.use_fp8, ctx.with_probs = use_fp8, probs is not None
-        ctx.probs_dtype = probs.dtype if probs is not None else None
-        ctx.probs_topk_stride, ctx.probs_row_width = probs_topk_stride, row_width
-
+    def forward(ctx, tokens, expert_map, num_local_experts, num_topk, pad_multiple, num_permuted_tokens,
+                scaling_factor, probs, scales_per_token, use_fp8, probs_topk_stride):
         if use_fp8 and scaling_factor is not None:
-            assert scales_per_token > 0, "scales_per_token must be > 0 when use_fp8=True"
+            assert scales_per_token > 0, "fp8 scaling factors need scales_per_token > 0"
         assert not (use_fp8 and probs is not None and tokens.requires_grad), (
-            "moe_permute: FP8 + probs backward is unsupported"
+            "moe_permute: fp8 tokens with probs have no backward"
         )
-
+        T = int(tokens.shape[0])
+        stride = int(probs_topk_stride) if probs is not None else 0
+        r, tpe, ovf = _route(expert_map, T, num_local_experts, num_topk, pad_multiple, num_permuted_tokens,
+                             stride, tokens.device)
+        # the row count is a host value: the cap, or the padded total (one host
+        # read); no tokens, no rows
         if T == 0:
-            row_id_map = torch.zeros((pad_multiple, 2 * num_local_experts + 1), dtype=torch.int32, device=dev)
-            tpe = torch.zeros((num_local_experts,), dtype=torch.int64, device=dev)
-            overflow = torch.zeros((1,), dtype=torch.int32, device=dev)
-            ndisp = torch.zeros((1,), dtype=torch.int32, device=dev)
-            out = tokens.new_empty((0, H))
-            osf = (scaling_factor.new_empty((0, scales_per_token))
-                   if use_fp8 and scaling_factor is not None else None)
-            opr = probs.new_zeros((0,)) if probs is not None else None
-            ctx.save_for_backward(row_id_map, ndisp)
-            return out, row_id_map, tpe, overflow, ndisp, osf, opr
-
-        row_id_map, tpe, overflow, ndisp = permute_preprocessing_impl(
-            expert_map, num_local_experts, num_topk, pad_multiple, num_permuted_tokens, probs_topk_stride
-        )
-        # the output row count is a host value: the cap, or the padded total (one host sync)
-        P = int(num_permuted_tokens) if num_permuted_tokens > 0 else int(tpe.sum().item())
-        out = torch.empty((P, H), dtype=tokens.dtype, device=dev)
-        osf = (torch.empty((P, scales_per_token), dtype=scaling_factor.dtype, device=dev)
-               if use_fp8 and scaling_factor is not None else None)
-        opr = torch.empty((P,), dtype=probs.dtype, device=dev) if probs is not None else None
-        permute_impl(tokens.contiguous(), out, scaling_factor, osf, probs, opr, row_id_map, ndisp, pad_multiple,
-                     num_local_experts, H, scales_per_token, use_fp8, probs is not None, P, probs_topk_stride)
-        ctx.save_for_backward(row_id_map, ndisp)
-        return out, row_id_map, tpe, overflow, ndisp, osf, opr
+            n_rows = 0
+        elif num_permuted_tokens > 0:
+            n_rows = int(num_permuted_tokens)
+        else:
+            n_rows = int(tpe.sum().item())
+        sf = scaling_factor if use_fp8 else None
+        rows, out_probs, out_sf = _expert_major(r, tokens, n_rows, probs, sf, scales_per_token, use_fp8)
+        _save(ctx, r)
+        ctx.n_tokens, ctx.fp8, ctx.has_probs = T, use_fp8, probs is not None
+        return rows, r.row_id_map, tpe, ovf, r.num_dispatched, out_sf, out_probs
 
     @staticmethod
-    def backward(ctx, g_out, g_rim, g_tpe, g_ovf, g_nd, g_sf, g_probs):
-        assert not ctx.use_fp8, "_MoEPermute.backward: FP8 backward not supported"
-        row_id_map, ndisp = ctx.saved_tensors
-        g_out = g_out.contiguous()
-        dev = g_out.device
-        g_tokens = torch.empty((ctx.num_dispatched, ctx.hidden_size), dtype=g_out.dtype, device=dev)
-        if ctx.with_probs and g_probs is not None:
-            g_probs = g_probs.contiguous()
-            g_in_probs = torch.empty((ctx.num_dispatched, ctx.probs_row_width), dtype=ctx.probs_dtype, device=dev)
-        else:
-            g_probs, g_in_probs = None, None
-        if ctx.num_dispatched > 0:
-            unpermute_impl(g_out, g_tokens, g_probs, g_in_probs, row_id_map, ndisp, ctx.num_local_experts,
-                           ctx.hidden_size, g_in_probs is not None, ctx.probs_topk_stride)
+    def backward(ctx, g_rows, _g_map, _g_tpe, _g_ovf, _g_nd, _g_sf, g_probs):
+        assert not ctx.fp8, "moe_permute: fp8 tokens have no backward"
+        g_probs = g_probs if ctx.has_probs else None
+        g_tokens, g_in_probs = _token_major(_load(ctx), g_rows, ctx.n_tokens, g_probs)
         return g_tokens, None, None, None, None, None, None, g_in_probs, None, None, None
 
 
-class _MoEUnpermute(torch.autograd.Function):
-    """Forward: gather-reduce.  Backward: scatter of the gradient (+ probs
-    gradient) (moe_permute.py:221-350)."""
+class _Unpermute(torch.autograd.Function):
+    """Forward gathers expert-major rows back per token; backward scatters
+    the token gradients (and the probs gradient) expert-major again."""
 
     @staticmethod
-    def forward(ctx, permuted_tokens, row_id_map, ndisp, restore_shape, num_local_experts, permuted_probs,
-                probs_topk_stride, pad_multiple):
-        dev = permuted_tokens.device
-        P = int(permuted_tokens.shape[0])
-        T, H = int(restore_shape[0]), int(restore_shape[1])
-        row_width = probs_topk_stride if probs_topk_stride > 0 else num_local_experts
-        ctx.num_permuted, ctx.hidden_size, ctx.num_local_experts = P, H, num_local_experts
-        ctx.with_probs = permuted_probs is not None
-        ctx.permuted_probs_dtype = permuted_probs.dtype if permuted_probs is not None else None
-        ctx.probs_topk_stride, ctx.probs_row_width, ctx.pad_multiple = probs_topk_stride, row_width, pad_multiple
-        out = torch.empty((T, H), dtype=permuted_tokens.dtype, device=dev)
-        oprobs = (torch.empty((T, row_width), dtype=permuted_probs.dtype, device=dev)
-                  if permuted_probs is not None else None)
-        ctx.save_for_backward(row_id_map, ndisp)
-        if P == 0 or T == 0:
-            return out, oprobs
-        unpermute_impl(permuted_tokens.contiguous(), out,
-                       permuted_probs.contiguous() if permuted_probs is not None else None, oprobs, row_id_map,
-                       ndisp, num_local_experts, H, permuted_probs is not None, probs_topk_stride)
-        return out, oprobs
+    def forward(ctx, permuted_tokens, row_id_map, num_dispatched, restore_shape, num_local_experts,
+                permuted_probs, probs_topk_stride, pad_multiple):
+        r = _Routing(row_id_map, num_dispatched, num_local_experts, pad_multiple, int(probs_topk_stride))
+        tokens, probs = _token_major(r, permuted_tokens, int(restore_shape[0]), permuted_probs)
+        _save(ctx, r)
+        ctx.n_rows, ctx.has_probs = int(permuted_tokens.shape[0]), permuted_probs is not None
+        return tokens, probs
 
     @staticmethod
-    def backward(ctx, g_out, g_oprobs):
-        row_id_map, ndisp = ctx.saved_tensors
-        g_out = g_out.contiguous()
-        dev = g_out.device
-        # padding rows of the gradient are written as zeros by the scatter itself
-        g_perm = torch.empty((ctx.num_permuted, ctx.hidden_size), dtype=g_out.dtype, device=dev)
-        if ctx.with_probs and g_oprobs is not None:
-            g_oprobs = g_oprobs.contiguous()
-            g_pprobs = torch.empty((ctx.num_permuted,), dtype=ctx.permuted_probs_dtype, device=dev)
-        else:
-            g_oprobs, g_pprobs = None, None
-        if ctx.num_permuted > 0 and g_out.shape[0] > 0:
-            permute_impl(g_out, g_perm, None, None, g_oprobs, g_pprobs, row_id_map, ndisp, ctx.pad_multiple,
-                         ctx.num_local_experts, ctx.hidden_size, 0, False, g_pprobs is not None, ctx.num_permuted,
-                         ctx.probs_topk_stride)
-        return g_perm, None, None, None, None, g_pprobs, None, None
+    def backward(ctx, g_tokens, g_probs):
+        g_probs = g_probs if ctx.has_probs else None
+        g_rows, g_row_probs, _ = _expert_major(_load(ctx), g_tokens, ctx.n_rows, g_probs)
+        return g_rows, None, None, None, None, g_row_probs, None, None
 
 
 def moe_permute(
@@ -150,21 +175,26 @@ def moe_permute(
     use_fp8: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor],
            Optional[torch.Tensor]]:
-    """Fused preprocessing + permute (moe_permute.py:353-393).
+    """Fused slot assignment + permute (reference moe_permute.py:353-393).
 
     ``expert_map`` is a bool routing map [T, num_local_experts] or top-k
     expert indices [T, num_topk] (int32/int64; entries outside
-    [0, num_local_experts) are ignored).  Returns (permuted_tokens,
-    row_id_map, tokens_per_expert, overflow_flag, num_dispatched_tokens,
+    [0, num_local_experts) are ignored).  ``probs_layout`` "topk" reads probs
+    as [T, num_topk] aligned with the index map, "routing_map" as
+    [T, num_local_experts].  Returns (permuted_tokens, row_id_map,
+    tokens_per_expert, overflow_flag, num_dispatched_tokens,
     permuted_scaling_factor, permuted_probs); pass ``num_dispatched_tokens``
-    straight to ``moe_unpermute``."""
-    if probs_layout not in ("routing_map", "topk"):
-        raise ValueError(f"moe_permute: probs_layout must be 'routing_map' or 'topk', got {probs_layout!r}")
-    if probs_layout == "topk" and num_topk <= 0:
-        raise ValueError("moe_permute: probs_layout='topk' requires num_topk > 0")
-    probs_topk_stride = num_topk if probs_layout == "topk" else 0
-    return _MoEPermute.apply(tokens, expert_map, num_local_experts, num_topk, pad_multiple, num_permuted_tokens,
-                             scaling_factor, probs, scales_per_token, use_fp8, probs_topk_stride)
+    straight to ``moe_unpermute``.  A bad ``probs_layout`` raises ValueError."""
+    if probs_layout == "topk":
+        if num_topk <= 0:
+            raise ValueError(f"moe_permute: probs_layout 'topk' needs num_topk > 0 (got {num_topk})")
+        stride = num_topk
+    elif probs_layout == "routing_map":
+        stride = 0
+    else:
+        raise ValueError(f"moe_permute: unknown probs_layout {probs_layout!r} (expected 'topk' or 'routing_map')")
+    return _Permute.apply(tokens, expert_map, num_local_experts, num_topk, pad_multiple, num_permuted_tokens,
+                          scaling_factor, probs, scales_per_token, use_fp8, stride)
 
 
 def moe_unpermute(
@@ -178,9 +208,11 @@ def moe_unpermute(
     probs_topk_stride: int = 0,
     pad_multiple: int = 0,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """Unpermute back into ``restore_shape`` (= the permuted input's shape)
-    (moe_permute.py:396-420).  ``probs_topk_stride`` selects the width of
-    ``unpermuted_probs`` (0: [T, num_local_experts], > 0: [T, stride]) and
-    ``pad_multiple`` must equal the forward's (it is used by the backward)."""
-    return _MoEUnpermute.apply(permuted_tokens, row_id_map, num_dispatched_tokens_tensor, restore_shape,
-                               num_local_experts, permuted_probs, probs_topk_stride, pad_multiple)
+    """Unpermute back into ``restore_shape`` (the permuted tokens' original
+    [T, hidden] shape) (reference moe_permute.py:396-420).
+    ``probs_topk_stride`` selects the width of the returned probs (0:
+    [T, num_local_experts], > 0: [T, stride]); ``pad_multiple`` must equal the
+    forward's (the backward scatter lays out the padding rows with it).  Every
+    output row is written, zero for tokens with no routed row."""
+    return _Unpermute.apply(permuted_tokens, row_id_map, num_dispatched_tokens_tensor, restore_shape,
+                            num_local_experts, permuted_probs, probs_topk_stride, pad_multiple)

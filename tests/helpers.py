@@ -75,6 +75,12 @@ def ref_lib():
             L.ref_moe_unpermute.argtypes = [vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, vp]
         else:  # an older build of oracle/_ref without the MoE permutation kernels
             L.ref_moe_preprocess = None
+        if hasattr(L, "ref_dequant_mxfp8"):
+            L.ref_dequant_mxfp8.argtypes = [vp, i32, i64, i64, vp, i64, i64, i32, vp, i32, vp]
+            L.ref_transpose_2d.argtypes = [vp, vp, i64, i64, i64, i64, vp]
+        else:  # an older build of oracle/_ref without the MX dequant / transpose kernels
+            L.ref_dequant_mxfp8 = None
+            L.ref_transpose_2d = None
         _ref = L
     return _ref
 

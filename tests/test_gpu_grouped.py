@@ -65,6 +65,15 @@ def test_grouped_blockwise_fwd_vs_oracle(lens, trans_b):
         off += L
 
 
+def _poison_pool(shape, dtype, sentinel=12288.0, n=24):
+    """Fill and free caching-allocator blocks of `shape` with a non-zero
+    sentinel, so the next allocation of that shape reuses a dirty block instead
+    of a fresh (zeroed) page and an unwritten output row shows up."""
+    blocks = [torch.full(shape, sentinel, dtype=dtype, device="cuda") for _ in range(n)]
+    torch.cuda.synchronize()
+    del blocks
+
+
 @pytest.mark.parametrize("lens", LENS)
 def test_grouped_tail_is_zero(lens):
     (turbo, _, _, SG, SR, gg, _, offs_from, segq) = _mods()
@@ -77,6 +86,7 @@ def test_grouped_tail_is_zero(lens):
     go = offs_from(gl)
     qa, sa = turbo.ops.quantize_fp8(a, torch.float8_e4m3fn, SG.TENSORWISE)
     qw, sw = turbo.ops.quantize_fp8(w, torch.float8_e4m3fn, SG.TENSORWISE)
+    _poison_pool((Mtot, N), torch.bfloat16)
     out = gg(qa, qw, sa, sw, gl, go, False, True, torch.bfloat16, SG.TENSORWISE.value)
     assert torch.all(out[M:] == 0)
     da = O.dequant_tensorwise(u8(qa), 0, f32(sa))
@@ -114,6 +124,48 @@ def test_grouped_variable_k_blockwise_vs_oracle(lens, trans_c):
             continue
         ref = O.gemm_ref(da[s:e], dg[s:e], True, False, trans_c)
         _check(o[g], ref, f"group {g}")
+
+
+@pytest.mark.parametrize("ori_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_grouped_padded_tail_zeroed_reference_case(ori_dtype, trans_b):
+    """The reference's padded-tail case (test_grouped_gemm_fp8.py:1073-1132):
+    G=8, K=2048, N=2880, lens [4096,0,3072,0,0,5120,0,0] plus 224 over-allocated
+    rows; after the allocator pool is poisoned with 12288.0 the tail of the
+    public op's output must be exactly zero."""
+    (turbo, QC, Fmt, SG, _, _, _, _, _) = _mods()
+    torch.manual_seed(42)
+    G, K, N = 8, 2048, 2880
+    gl = torch.tensor([4096, 0, 3072, 0, 0, 5120, 0, 0], dtype=torch.int64, device="cuda")
+    S = int(gl.sum())
+    Mt = S + 224
+    cfg = QC(format=Fmt.E4M3, granularity=SG.TENSORWISE)
+    a = torch.randn((Mt, K), dtype=ori_dtype, device="cuda")
+    b = torch.randn((G, N, K) if trans_b else (G, K, N), dtype=ori_dtype, device="cuda")
+    turbo.ops.grouped_gemm_fp8(a, b, gl, trans_b=trans_b, config=cfg)
+    torch.cuda.synchronize()
+    _poison_pool((Mt, N), ori_dtype)
+    out = turbo.ops.grouped_gemm_fp8(a, b, gl, trans_b=trans_b, config=cfg)
+    torch.cuda.synchronize()
+    tail = out[S:Mt]
+    assert torch.isfinite(tail).all()
+    assert torch.count_nonzero(tail).item() == 0
+
+
+def test_grouped_variable_k_blockwise_rejects_unaligned_segments():
+    """BLOCKWISE column scales hold one row per 128 padded rows, so segments
+    that are not 128-aligned cannot be indexed: the call raises instead of
+    reading the wrong scale rows."""
+    (turbo, _, _, SG, _, _, gvk, offs_from, _) = _mods()
+    lens = [100, 156]
+    M, K, N = sum(lens), 256, 128
+    a8 = torch.zeros((M, K), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+    g8 = torch.zeros((M, N), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+    sa = torch.ones((2, K), device="cuda")
+    sg = torch.ones((2, N), device="cuda")
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    with pytest.raises(RuntimeError, match="128-aligned"):
+        gvk(a8, g8, sa, sg, gl, offs_from(gl), True, False, False, torch.bfloat16, SG.BLOCKWISE.value)
 
 
 def _lens_many(G, seed):
@@ -487,15 +539,17 @@ def _ref_group_lens(b, m, seed):
     return lens
 
 
-@pytest.mark.parametrize("B,M", [(1, 256), (3, 512), (8, 128), (16, 256)])
-@pytest.mark.parametrize("NK", [(2048, 1408), (1408, 2048)])
+@pytest.mark.parametrize("B,M", [(1, 256), (3, 512), (8, 128), (16, 256), (32, 128), (32, 2048)])
+@pytest.mark.parametrize("NK", [(2048, 1408), (1408, 2048), (4096, 7168), (7168, 2048)])
 @pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
 @pytest.mark.parametrize("fmt", ["E4M3", "E5M2"])
 @pytest.mark.parametrize("trans_b", [True, False])
 def test_grouped_reference_grid(B, M, NK, gran, fmt, trans_b):
     """A slice of the reference's grouped grid (test_grouped_gemm_fp8.py:35-50,
-    437-570: its B / M / (N, K) values, unbalanced splits, both formats and
-    weight layouts) at its SNR criterion: > 25 dB for e4m3, > 20 for e5m2."""
+    437-570: its B / M / (N, K) values including B = 32 and the DeepSeek-size
+    (4096, 7168) / (7168, 2048) pairs, unbalanced splits, both formats and
+    weight layouts) at its SNR criterion: > 25 dB for e4m3, > 20 for e5m2
+    (SNR computed on the GPU in fp64)."""
     (turbo, Cfg, Format, SG, _, _, _, _, _) = _mods()
     g = getattr(SG, gran)
     if g == SG.MX_BLOCKWISE and not trans_b:
@@ -524,5 +578,6 @@ def test_grouped_reference_grid(B, M, NK, gran, fmt, trans_b):
     ref.backward(grad.float())
     thr = 25 if fmt == "E4M3" else 20
     for name, x, r in (("out", out, ref), ("dA", a.grad, a_ref.grad), ("dB", b.grad, b_ref.grad)):
-        s = O.snr_db(f32(r), f32(x))
+        r64, x64 = r.detach().double(), x.detach().double()
+        s = float(10.0 * torch.log10(r64.pow(2).sum() / (r64 - x64).pow(2).sum().clamp_min(1e-300)))
         assert s > thr, f"{name} SNR {s:.1f} dB"

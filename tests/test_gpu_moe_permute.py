@@ -363,6 +363,37 @@ def test_moe_permute_empty_input(with_probs, pad):
     assert p0.grad is not None and p0.grad.shape == (0, H)
 
 
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64, torch.bool])
+@pytest.mark.parametrize("with_probs", [False, True])
+def test_moe_unpermute_nothing_routed_is_zero(dtype, with_probs):
+    """Every token routes outside [0, E) (or to no local expert): nothing is
+    dispatched, the permuted operand is empty, and the unpermuted tokens (and
+    probs) must come back exactly zero -- not whatever the allocator held.
+    The caching allocator is filled with a non-zero pattern first, so an
+    unwritten output row cannot pass by landing on a zeroed page."""
+    moe_permute, moe_unpermute = _ops()
+    T, E, H, k = 300, 8, 256, 2
+    if dtype == torch.bool:
+        em = torch.zeros((T, E), dtype=torch.bool, device="cuda")
+    else:
+        em = torch.randint(E, 3 * E, (T, k), dtype=dtype, device="cuda")
+        em[::3, 0] = -1
+    layout = "routing_map" if dtype == torch.bool else "topk"
+    tok = randn((T, H)).cuda()
+    probs = torch.rand((T, E if dtype == torch.bool else k), device="cuda") if with_probs else None
+    perm, rim, tpe, ovf, nd, _, pp = moe_permute(tok, em, num_local_experts=E, num_topk=0 if dtype == torch.bool else k,
+                                                 probs=probs, probs_layout=layout)
+    assert perm.shape == (0, H) and int(tpe.sum().item()) == 0 and int(nd.item()) == 0
+    junk = torch.full((8 << 20,), 0x3F80, dtype=torch.int16, device="cuda")  # bf16 1.0 everywhere
+    del junk
+    u, up = moe_unpermute(perm, rim, nd, restore_shape=tok.shape, num_local_experts=E, permuted_probs=pp,
+                          probs_topk_stride=0 if dtype == torch.bool else k)
+    torch.cuda.synchronize()
+    assert u.shape == (T, H) and torch.count_nonzero(u).item() == 0
+    if with_probs:
+        assert torch.count_nonzero(up).item() == 0
+
+
 def _layout(rm, pad):
     T, E = rm.shape
     real = rm.sum(0).tolist()

@@ -188,29 +188,63 @@ def test_segment_equals_block1d_on_padded_groups():
 
 @pytest.mark.parametrize("fmt,emax", [(0, 8), (1, 15)])
 def test_mx_exponent_rule(fmt, emax):
-    for amax in [1.0, 1.5, 2.0, 447.0, 448.0, 3e-5, 1e30, 2.0 ** -126, 2.0 ** -130]:
-        e = O.mx_e8m0(amax, fmt)
-        exp = int(np.floor(np.log2(amax))) - emax + 127
-        assert e == min(max(exp, 0), 254), amax
+    """E = floor(log2 amax) - emax, plus 1 when the mantissa of amax exceeds
+    1.75 (amax * 2^-E would exceed fp8_max = 1.75 * 2^emax), biased by 127 and
+    clamped to [0, 254]; restated here with float64 log2."""
+    fmax = O.FP8_MAX[fmt]
+    for amax in [1.0, 1.5, 1.75, 1.7500001, 1.76, 1.99, 2.0, 3.5, 3.51, 447.0, 448.0, 449.0, 3e-5, 1e30,
+                 2.0 ** -126, 1.9 * 2.0 ** -126, 2.0 ** -130, fmax, fmax * 1.0001, 3.4e38]:
+        a32 = float(np.float32(amax))
+        fl = int(np.floor(np.log2(a32)))
+        bump = 1 if a32 / 2.0 ** fl > 1.75 else 0
+        exp = fl - emax + bump + 127
+        assert O.mx_e8m0(a32, fmt) == min(max(exp, 0), 254), amax
     assert O.mx_e8m0(0.0, fmt) == 0
     x = (torch.exp(torch.randn(64, 256, generator=torch.Generator().manual_seed(7)) * 3)).to(torch.bfloat16)
     q, e = O.quant_mx(x, fmt, 1)
     assert q.shape == (64, 256) and e.shape == (64, 8)
     y = O.dequant_mx(q, fmt, e)
     xf = O.to_float32(x).astype(np.float64)
-    # the block max lands in the top binade of the element format
     sc = O.e8m0_to_scale(e).astype(np.float64)
-    blk = np.abs(y).reshape(64, 8, 32).max(-1)
-    assert np.all(blk >= 2.0 ** emax * sc)
-    # every element is the RNE value of x / scale (half a quantum, or half the
-    # smallest subnormal), unless it was clamped to +-max
-    mbits, bias = (3, 7) if fmt == 0 else (2, 15)
     s_full = np.repeat(sc, 32, axis=1)
+    # nothing saturates, and the block max lands in the top binade below fp8_max
+    assert np.all(np.abs(xf) / s_full <= fmax)
+    blk = np.abs(xf).reshape(64, 8, 32).max(-1) / sc
+    assert np.all((blk > fmax / 2) & (blk <= fmax))
+    # every element is the RNE value of x / scale (half a quantum, or half the
+    # smallest subnormal)
+    mbits, bias = (3, 7) if fmt == 0 else (2, 15)
     v = np.abs(xf) / s_full
     half_q = np.maximum(2.0 ** (np.floor(np.log2(np.maximum(v, 1e-300))) - mbits - 1), 2.0 ** (1 - bias - mbits - 1))
     err = np.abs(y - xf) / s_full
-    clamped = np.abs(y) / s_full == O.FP8_MAX[fmt]
-    assert np.all((err <= half_q * (1 + 1e-12)) | clamped)
+    assert np.all(err <= half_q * (1 + 1e-12))
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("use_2d", [False, True])
+def test_mx_rule_meets_reference_roundtrip_and_floor_rule_does_not(fmt, use_2d):
+    """The reference's MX round-trip criterion (test_quantization.py:304-460:
+    |x - dq(q(x))| <= 0.1 + 0.1 |dq(q(x))| on 1024 x 1024 N(0,1) inputs) holds
+    for the oracle's rule, while the plain OCP floor rule (no bump, so block
+    maxima with mantissa above 1.75 clamp to +-fp8_max) breaks it on the same
+    input.  The planted rule lives here, on the CPU, only as the counter-case."""
+    x = torch.randn(1024, 1024, generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
+    xf = O.to_float32(x).astype(np.float64)
+    q, e = O.quant_mx(x, fmt, 1, use_2d)
+    y = O.dequant_mx(q, fmt, e)
+    assert np.all(np.abs(xf - y) <= 0.1 + 0.1 * np.abs(y))
+    # counter-case: floor rule; saturated elements dequantize to +-fp8_max * 2^E
+    fmax, emax = O.FP8_MAX[fmt], (8 if fmt == 0 else 15)
+    blocks = np.abs(xf).reshape(32, 32, 32, 32).max(axis=(1, 3)) if use_2d else np.abs(xf).reshape(1024, 32, 32).max(-1)
+    E = np.floor(np.log2(blocks)) - emax
+    if use_2d:
+        E = np.repeat(np.repeat(E, 32, 0), 32, 1)
+    else:
+        E = np.repeat(E, 32, 1)
+    sat = np.abs(xf) * 2.0 ** -E > fmax
+    y_sat = np.sign(xf) * fmax * 2.0 ** E
+    bad = sat & (np.abs(xf - y_sat) > 0.1 + 0.1 * np.abs(y_sat))
+    assert bad.sum() > 0
 
 
 def test_mx_padding_and_transpose_layout():
