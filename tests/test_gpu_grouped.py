@@ -539,7 +539,7 @@ def _ref_group_lens(b, m, seed):
     return lens
 
 
-@pytest.mark.parametrize("B,M", [(1, 256), (3, 512), (8, 128), (16, 256), (32, 128), (32, 2048)])
+@pytest.mark.parametrize("B,M", [(1, 256), (3, 512), (8, 128), (16, 256), (32, 128)])
 @pytest.mark.parametrize("NK", [(2048, 1408), (1408, 2048), (4096, 7168), (7168, 2048)])
 @pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
 @pytest.mark.parametrize("fmt", ["E4M3", "E5M2"])
