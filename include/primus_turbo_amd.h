@@ -70,6 +70,18 @@ int pta_quantize_fp8_tensorwise(const void *x, int in_dtype, int64_t n, const fl
                                 void *q, int fmt, float *scale_inv, void *workspace,
                                 size_t workspace_bytes, pta_stream_t stream);
 
+/* Allocation-free variant of pta_quantize_fp8_tensorwise (same arguments
+ * without the workspace, same results).  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The amax
+ * pass keeps its partial maxima (at most 2048 floats for any n) in a static
+ * device array of PTA_TENSORWISE_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends; the call itself allocates nothing.  Calls that overlap on one
+ * GPU share that array and race. */
+#define PTA_TENSORWISE_NOALLOC_SCRATCH_BYTES 8192
+int pta_quantize_fp8_tensorwise_noalloc(const void *x, int in_dtype, int64_t n, const float *scale,
+                                        void *q, int fmt, float *scale_inv, pta_stream_t stream);
+
 /* Workspace bytes needed by pta_quantize_fp8_rowwise. */
 size_t pta_quantize_fp8_rowwise_workspace_size(int64_t outer, int64_t len, int64_t inner);
 

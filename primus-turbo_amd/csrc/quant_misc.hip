@@ -6,11 +6,15 @@
 //   quant op                  csrc/include/primus_turbo/device/quant_utils.cuh:31-38
 //   rowwise (row-major)       csrc/kernels/quantization/quantization_rowwise.cu:57-135
 //   rowwise (other axis)      csrc/kernels/quantization/quantization_rowwise.cu:186-235
-// The MX rule (kernel source absent from the reference snapshot) is the OCP
-// MX v1.0 shared-exponent rule encoded by the constants of
-// csrc/include/primus_turbo/quantization.h:88-102:
-//   e8m0 = clamp(biased_exp(amax) - emax_elem, 0, 254), q = fp8(x * 2^(127 - e8m0)).
+// The MX rule (kernel source absent from the reference snapshot) follows the
+// constants of csrc/include/primus_turbo/quantization.h:85-102 and the
+// reference's MX round-trip test (tests/pytorch/ops/test_quantization.py:
+// 304-460), which rules out saturating block maxima:
+//   E = floor(log2 amax) - emax_elem, plus 1 when amax * 2^-E > fp8_max,
+//   e8m0 = clamp(E + 127, 0, 254), q = fp8(x * 2^(127 - e8m0)).
 #include "common.h"
+
+#include <mutex>
 
 namespace pta {
 namespace {
@@ -909,4 +913,63 @@ extern "C" int pta_transpose_u8(const void *x, int64_t B, int64_t M, int64_t N, 
                                                             static_cast<uint8_t *>(y));
     PTA_CHECK_LAUNCH();
     return PTA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free tensorwise quantization.  This entry point has no
+// counterpart in the reference: it serves callers that cannot allocate device
+// memory (code under HIP graph capture, tight serving loops, harnesses that
+// forbid hipMalloc).  The amax pass's partial maxima (at most TW_MAX_PARTS
+// floats for any n) live in `scratch`, a file-scope device array of
+// TW_MAX_PARTS * 4 = 8 KiB that every GPU the library runs on holds until the
+// process ends.  The amax kernel writes every partial the quant kernel reads,
+// so nothing has to start at zero.  All calls on one GPU share that GPU's
+// array: calls that overlap on one GPU (different streams, or host threads
+// without ordering) race on it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[pta::TW_MAX_PARTS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex    g_scratch_mu;
+float        *g_scratch_ptr[kMaxDevices] = {}; // device address of `scratch` per device
+
+// Device address of this GPU's `scratch`, looked up once per device with that
+// device current.  The array's name in host code is only a stand-in for the
+// symbol; kernels and copies get this pointer instead.
+int scratch_for_current_device(float **out) {
+    int dev = -1;
+    PTA_CHECK_HIP(hipGetDevice(&dev));
+    PTA_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device index %d outside the supported range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        PTA_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        PTA_CHECK_ARG(p != nullptr, "no device address for the scratch array on device %d", dev);
+        g_scratch_ptr[dev] = static_cast<float *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return PTA_OK;
+}
+} // namespace
+
+static_assert(sizeof(float) * pta::TW_MAX_PARTS == PTA_TENSORWISE_NOALLOC_SCRATCH_BYTES,
+              "the header states the scratch size");
+
+extern "C" int pta_quantize_fp8_tensorwise_noalloc(const void *x, int in_dtype, int64_t n, const float *scale,
+                                                   void *q, int fmt, float *scale_inv, pta_stream_t stream) {
+    clear_error();
+    if (int rc = check_in(x, in_dtype, fmt)) return rc;
+    PTA_CHECK_ARG(q && scale_inv && n >= 0, "bad arguments");
+    float *parts = nullptr;
+    if (scale == nullptr) {
+        // the amax pass writes one partial per workgroup: tw_grid(n) <= TW_MAX_PARTS
+        const int g = tw_grid(n);
+        PTA_CHECK_ARG(g <= TW_MAX_PARTS, "tensorwise amax needs %d partials, the scratch holds %d", g,
+                      TW_MAX_PARTS);
+        if (int rc = scratch_for_current_device(&parts)) return rc;
+    }
+    const bool vec = aligned16(x) && aligned16(q);
+    return PTA_DISPATCH_IN_FMT(in_dtype, fmt, tw_launch, x, n, scale, static_cast<uint8_t *>(q), scale_inv, parts,
+                               vec, as_stream(stream));
 }

@@ -34,6 +34,7 @@ SIGNATURES = {
     "pta_abi_version": (_i32, []),
     "pta_quantize_fp8_tensorwise_workspace_size": (_sz, [_i64]),
     "pta_quantize_fp8_tensorwise": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
+    "pta_quantize_fp8_tensorwise_noalloc": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp, _vp]),
     "pta_quantize_fp8_rowwise_workspace_size": (_sz, [_i64, _i64, _i64]),
     "pta_quantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
     "pta_quantize_fp8_blockwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),
