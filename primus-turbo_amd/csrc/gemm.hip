@@ -1,6 +1,19 @@
 // Host side of the dense FP8 GEMM: layout reduction to NT and scale-stride
 // bookkeeping (the kernel itself lives in gemm_kernel.h).
 #include "gemm_kernel.h"
+#include "gemm_small.h"
+
+// Problems with fewer 256 x 256 tiles than this run on the 64 x 64-tile kernel
+// (gemm_small.h), which also reads K-major operands without a transpose pass.
+// Measured crossovers on MI355X: NT 2048^3 (64 tiles) 21 us small vs 24 us
+// large, 1536 x 4096 x 4096 (96 tiles) 47 vs 44; with a K-major operand the
+// large kernel also pays the transpose (1024 x 4096 x 4096 NN: 74 vs 125).
+#ifndef PTA_SMALL_MAX_TILES
+#define PTA_SMALL_MAX_TILES 72
+#endif
+#ifndef PTA_SMALL_MAX_TILES_KMAJOR
+#define PTA_SMALL_MAX_TILES_KMAJOR 100
+#endif
 
 namespace pta {
 using namespace gemm_detail;
@@ -53,10 +66,76 @@ __global__ void zero_fill_kernel(uint8_t *c, int64_t bytes) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes; i += stride) c[i] = 0;
 }
+
+// pta_gemm_fp8 on the small-tile kernel: operands read in place (K-major for
+// trans_a A and for non-trans_b B), scale strides as the reference's layouts
+// give them, C^T by exchanging the operands.
+int gemm_small_nt(const void *a, int a_fmt, const void *a_scale, int trans_a, const void *b, int b_fmt,
+                  const void *b_scale, int trans_b, void *c, int c_dtype, int trans_c, int64_t M, int64_t N,
+                  int64_t K, int sm, hipStream_t st) {
+    using gemm_small::SmallArgs;
+    const int64_t kb = cdiv(K, 128);
+    SmallArgs     g{};
+    g.a = static_cast<const uint8_t *>(a); g.b = static_cast<const uint8_t *>(b); g.c = c;
+    g.M = M; g.N = N; g.K = K;
+    g.lda = trans_a ? M : K; // A [K, M] or [M, K]
+    g.ldb = trans_b ? K : N; // B [N, K] or [K, N]
+    g.ldc = N;
+    g.sa = a_scale; g.sb = b_scale;
+    g.sa_bytes = 4; g.sb_bytes = 4;
+    if (sm == SM_ROW) { g.sa_bytes = M * 4; g.sb_bytes = N * 4; }
+    if (sm == SM_BLOCK) {
+        // A: [M, K/128] or [K/128, M]; B: [N/128, K/128] (NT), [K/128, N/128] (NN), [K/128, N] (TN)
+        if (!trans_a) { g.sa_m = kb; g.sa_k = 1; } else { g.sa_m = 1; g.sa_k = M; }
+        if (trans_b) { g.b2d = 1; g.sb_m = kb; g.sb_k = 1; }
+        else if (!trans_a) { g.b2d = 1; g.sb_m = 1; g.sb_k = cdiv(N, 128); }
+        else { g.b2d = 0; g.sb_m = 1; g.sb_k = N; }
+        g.sa_bytes = M * kb * 4;
+        g.sb_bytes = (g.b2d ? cdiv(N, 128) : N) * kb * 4;
+    }
+    if (sm == SM_MX) {
+        g.sa_m = K / 32; g.sb_m = K / 32; g.sa_k = 4; g.sb_k = 4;
+        g.sa_bytes = M * (K / 32); g.sb_bytes = N * (K / 32);
+    }
+    bool akm = trans_a != 0, bkm = trans_b == 0;
+    int  fa = a_fmt, fb = b_fmt;
+    if (trans_c) { // C^T[n, m] = sum_k B(n, k) A(m, k)
+        std::swap(g.a, g.b); std::swap(g.lda, g.ldb); std::swap(g.M, g.N);
+        std::swap(g.sa, g.sb); std::swap(g.sa_m, g.sb_m); std::swap(g.sa_k, g.sb_k);
+        std::swap(g.sa_bytes, g.sb_bytes); std::swap(g.a2d, g.b2d);
+        std::swap(akm, bkm); std::swap(fa, fb);
+        g.ldc = M;
+    }
+    g.tiles_m = static_cast<int>(cdiv(g.M, gemm_small::SBM));
+    g.tiles_n = static_cast<int>(cdiv(g.N, gemm_small::SBN));
+    // about square per-XCD tile blocks: group_m = 2^floor(log2(sqrt(tiles / 8)))
+    g.group_m = 1;
+    while (4 * g.group_m * g.group_m * 8 <= int64_t(g.tiles_m) * g.tiles_n && 2 * g.group_m <= g.tiles_m) g.group_m *= 2;
+    g.aligned_c = ((g.ldc * (c_dtype == PTA_F32 ? 4 : 2)) % 16 == 0) && aligned16(c);
+    switch (sm) {
+    case SM_TENSOR: return gemm_small::dispatch_small_tensor(g, akm, bkm, fa, fb, c_dtype, st);
+    case SM_ROW: return gemm_small::dispatch_small_row(g, akm, bkm, fa, fb, c_dtype, st);
+    case SM_BLOCK: return gemm_small::dispatch_small_block(g, akm, bkm, fa, fb, c_dtype, st);
+    default: return gemm_small::dispatch_small_mx(g, fa, fb, c_dtype, st);
+    }
+}
 } // namespace
+
+// Whether pta_gemm_fp8 takes the small-tile kernel: few large tiles, K-major
+// operands with a row stride that is a multiple of 8 (8-byte K-row loads), and
+// every operand offset of the kernel within 32 bits.
+static bool small_path(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b) {
+    const bool kmajor = trans_a || !trans_b;
+    if (cdiv(M, BM) * cdiv(N, BN) >= (kmajor ? PTA_SMALL_MAX_TILES_KMAJOR : PTA_SMALL_MAX_TILES)) return false;
+    const int64_t lim = int64_t(1) << 30;
+    if (trans_a ? (M % 8 != 0 || (K + 1024) * M >= lim) : 64 * K >= lim) return false;
+    if (!trans_b ? (N % 8 != 0 || (K + 1024) * N >= lim) : 64 * K >= lim) return false;
+    return true;
+}
 
 extern "C" size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, int trans_a,
                                               int trans_b, int /*granularity*/) {
+    if (small_path(M, N, K, trans_a, trans_b)) return 0;
     size_t ws = 0;
     if (trans_a) ws += static_cast<size_t>(cdiv(M * K, 256) * 256);
     if (!trans_b) ws += static_cast<size_t>(cdiv(N * K, 256) * 256);
@@ -93,6 +172,9 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
     const size_t need = pta_gemm_fp8_workspace_size(M, N, K, trans_a, trans_b, granularity);
     PTA_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                   "workspace of %zu bytes required", need);
+    if (small_path(M, N, K, trans_a, trans_b))
+        return gemm_small_nt(a, a_fmt, a_scale, trans_a, b, b_fmt, b_scale, trans_b, c, c_dtype, trans_c, M, N, K,
+                             sm, st);
 
     // ---- reduce to NT: A' [M, K] K-contiguous, B' [N, K] K-contiguous ------
     const uint8_t *ap = static_cast<const uint8_t *>(a);

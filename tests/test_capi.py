@@ -61,7 +61,13 @@ def test_workspace_queries():
     from primus_turbo.pytorch import _C
 
     assert _C.query("pta_gemm_fp8_workspace_size", 128, 256, 512, 0, 1, 3) == 0
-    assert _C.query("pta_gemm_fp8_workspace_size", 128, 256, 512, 1, 0, 3) >= 128 * 512 + 256 * 512
+    # few tiles: the small-tile kernel reads K-major operands in place
+    assert _C.query("pta_gemm_fp8_workspace_size", 128, 256, 512, 1, 0, 0) == 0
+    # unless a K-major row stride is not a multiple of 8 (then both are transposed)
+    assert _C.query("pta_gemm_fp8_workspace_size", 132, 256, 512, 1, 0, 0) >= 132 * 512 + 256 * 512
+    # many tiles: the large-tile kernel reads NT copies
+    assert _C.query("pta_gemm_fp8_workspace_size", 4096, 4096, 512, 1, 0, 0) >= 2 * 4096 * 512
+    assert _C.query("pta_gemm_fp8_workspace_size", 4096, 4096, 512, 0, 0, 0) >= 4096 * 512
     assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 4, 100, 1) == 0
     assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 1, 100, 64) > 0
 

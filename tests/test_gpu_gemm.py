@@ -40,7 +40,7 @@ def _check(out, ref, what):
     return snr, rel
 
 
-@pytest.mark.parametrize("mnk", [(512, 1024, 1024), (255, 512, 576), (1024, 768, 2048), (64, 128, 128)])
+@pytest.mark.parametrize("mnk", [(512, 1024, 1024), (255, 512, 576), (1024, 768, 2048), (64, 128, 128), (2304, 4096, 256)])
 @pytest.mark.parametrize("layout", ["NT", "NN", "TN"])
 @pytest.mark.parametrize("trans_c", [False, True])
 @pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE"])
