@@ -167,6 +167,41 @@ def _accuracy(seed_inputs, gpu_out):
             "reference": "fp64 product of the dequantized FP8 operands (CPU oracle), whole output"}
 
 
+def _quant_calls(a, w):
+    """Three calls of each BASELINE quantize kernel on its config's shape, for
+    the FETCH_SIZE / WRITE_SIZE counter passes (no timing)."""
+    import torch
+
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_dual_impl,
+        quant_fp8_blockwise_for_weight_impl,
+        quant_fp8_blockwise_segment_m_row_col_impl,
+        quantize_fp8_rowwise_impl,
+        quantize_mxfp8_impl,
+    )
+
+    e4 = torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(2)
+    dev = a.device
+    x2 = torch.randn((8192, 4096), generator=g).bfloat16().to(dev)
+    lens = _zipf_counts(65536, 32, 28, 0).to(dev)
+    offs = group_offs_from_lens(lens)
+    x4 = torch.randn((65536, 7168), generator=g).bfloat16().to(dev)
+    x5 = torch.randn((8192, 8192), generator=g).bfloat16().to(dev)
+    calls = [
+        lambda: quant_fp8_blockwise_dual_impl(a, e4, 128, col_transposed=True, row_scale_kmajor=True),
+        lambda: quant_fp8_blockwise_for_weight_impl(w, e4, 128),
+        lambda: quantize_fp8_rowwise_impl(x2, e4, -1),
+        lambda: quant_fp8_blockwise_segment_m_row_col_impl(x4, e4, 128, lens, offs),
+        lambda: quantize_mxfp8_impl(x5, e4, None, 32, with_trans=True, exp_kmajor=True),
+    ]
+    for f in calls:
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,8 +210,9 @@ def main():
     ap.add_argument("--settle-ms", type=float, default=60.0,
                     help="GPU milliseconds of untimed calls before the warm-up (the clock settles after input setup)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemm"], default="all",
-                    help="gemm: time only the headline GEMM (for counter passes)")
+    ap.add_argument("--only", choices=["all", "gemm", "quant"], default="all",
+                    help="gemm: time only the headline GEMM; quant: the headline GEMM, then three calls of each "
+                         "BASELINE quantize kernel (both for counter passes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with three 256 MiB device copies (reference for the FETCH/WRITE counters)")
     args = ap.parse_args()
@@ -230,6 +266,8 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
 
     extras = {}
+    if args.only == "quant":
+        _quant_calls(a, w)
     if args.only == "all":
         extras = _extras(args, a, w, grad, M, N, K, flops)
         del grad
