@@ -272,6 +272,7 @@ def main():
         extras = _extras(args, a, w, grad, M, N, K, flops)
         del grad
         extras["other_configs"] = _other_configs(args)
+        extras["vendor_reference"] = _vendor_reference(args, M, N, K)
 
     cpu, accuracy = None, None
     if not args.no_cpu_baseline:
@@ -339,6 +340,29 @@ def _quant_parity(a_cpu, w_cpu, a_q, a_s, w_q, w_s):
         "weight_128x128": bool(np.array_equal(qw, w_q) and np.array_equal(sw.view(np.uint32), w_s.view(np.uint32))),
         "reference": "CPU oracle (oracle/fp8_oracle.c), bytes and fp32 scale bits",
     }
+
+
+def _vendor_reference(args, M, N, K):
+    """The vendor library on the headline shape, for context (not `value`):
+    torch._scaled_mm (hipBLASLt) with e4m3 operands and tensorwise scales,
+    bf16 out. hipBLASLt has no 1x128 / 128x128 blockwise mode, so this is the
+    closest library kernel to the measured blockwise one; it skips the
+    per-K-block scale work the blockwise kernel does."""
+    import torch
+
+    e4 = torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(3)
+    try:
+        a = torch.randn((M, K), generator=g).to("cuda").to(e4)
+        b = torch.randn((N, K), generator=g).to("cuda").to(e4).t()  # K x N, column-major
+        one = torch.tensor(1.0, device="cuda")
+        fn = lambda: torch._scaled_mm(a, b, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)  # noqa: E731
+        ms = _time_settled(fn, max(20, args.steps // 2))
+    except Exception as exc:  # a torch build without the fp8 hipBLASLt path
+        return {"hipblaslt_tensorwise": None, "error": f"{type(exc).__name__}: {exc}"[:200]}
+    rec = _gemm_rec(ms, 2.0 * M * N * K)
+    rec["what"] = "torch._scaled_mm e4m3 tensorwise (hipBLASLt), same shape, bf16 out"
+    return {"hipblaslt_tensorwise": rec}
 
 
 def _gemm_rec(ms, flops):
