@@ -14,6 +14,17 @@
 #ifndef PTA_SMALL_MAX_TILES_KMAJOR
 #define PTA_SMALL_MAX_TILES_KMAJOR 100
 #endif
+// Tile of the small kernel: 128 x 128 when that still gives this many tiles,
+// else 64 x 64 when that does, else 32 x 64 (about one tile per CU or more).
+#ifndef PTA_SMALL_T128_MIN
+#define PTA_SMALL_T128_MIN 240
+#endif
+#ifndef PTA_SMALL_T64_MIN
+#define PTA_SMALL_T64_MIN 240
+#endif
+#ifndef PTA_SMALL_FORCE_TILE
+#define PTA_SMALL_FORCE_TILE -1
+#endif
 
 namespace pta {
 using namespace gemm_detail;
@@ -106,8 +117,22 @@ int gemm_small_nt(const void *a, int a_fmt, const void *a_scale, int trans_a, co
         std::swap(akm, bkm); std::swap(fa, fb);
         g.ldc = M;
     }
-    g.tiles_m = static_cast<int>(cdiv(g.M, gemm_small::SBM));
-    g.tiles_n = static_cast<int>(cdiv(g.N, gemm_small::SBN));
+    // the largest tile whose grid still covers the CUs (a K-major operand's
+    // row stride must be a multiple of the tile's bytes per K row and thread)
+    using gemm_small::TILE_32x64;
+    using gemm_small::TILE_64x64;
+    using gemm_small::TILE_128x128;
+    const int64_t t128 = cdiv(g.M, 128) * cdiv(g.N, 128), t64 = cdiv(g.M, 64) * cdiv(g.N, 64);
+    const bool    ok128 = (!akm || g.lda % 16 == 0) && (!bkm || g.ldb % 16 == 0);
+    g.tile = (t128 >= PTA_SMALL_T128_MIN && ok128) ? TILE_128x128 : (t64 >= PTA_SMALL_T64_MIN ? TILE_64x64 : TILE_32x64);
+#if PTA_SMALL_FORCE_TILE >= 0
+    g.tile = PTA_SMALL_FORCE_TILE;
+    if (g.tile == TILE_128x128 && !ok128) g.tile = TILE_64x64;
+#endif
+    const int tbm = g.tile == TILE_128x128 ? 128 : (g.tile == TILE_64x64 ? 64 : 32);
+    const int tbn = g.tile == TILE_128x128 ? 128 : 64;
+    g.tiles_m = static_cast<int>(cdiv(g.M, tbm));
+    g.tiles_n = static_cast<int>(cdiv(g.N, tbn));
     // about square per-XCD tile blocks: group_m = 2^floor(log2(sqrt(tiles / 8)))
     g.group_m = 1;
     while (4 * g.group_m * g.group_m * 8 <= int64_t(g.tiles_m) * g.tiles_n && 2 * g.group_m <= g.tiles_m) g.group_m *= 2;

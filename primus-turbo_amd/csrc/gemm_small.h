@@ -1,21 +1,21 @@
-// Small-problem FP8 GEMM for gfx950 (MI355X).
+// Small- and mid-size FP8 GEMM for gfx950 (MI355X).
 //
 // The large-tile kernel (gemm_kernel.h) gives each workgroup a 256 x 256 tile
-// and walks K serially; a problem with a handful of such tiles (512 x 1024,
-// say: 8 tiles) leaves almost every one of the 256 CUs idle and is bound by
-// the latency of its long K loop.  Here a workgroup of four waves owns a
-// 64 x 64 tile, so the same product runs on 16x as many workgroups, and either
-// operand may be read K-contiguous ([rows, K]) or K-major ([K, rows]): a
-// K-major tile is transposed in registers (4 x 4 byte blocks, v_perm) on its
+// and walks K serially; a problem with few such tiles (512 x 1024, say: 8
+// tiles) leaves most of the 256 CUs idle and is bound by the latency of its
+// long K loop.  Here a workgroup of four waves (2 x 2) owns a 32 x 64, 64 x 64
+// or 128 x 128 tile (chosen per problem so the grid covers the CUs), and
+// either operand may be read K-contiguous ([rows, K]) or K-major ([K, rows]):
+// a K-major tile is transposed in registers (4 x 4 byte blocks, v_perm) on its
 // way into LDS, so the NN and TN layouts need no separate transpose pass.
 //
 // Pipeline, per thread: RING K blocks (128 deep) of both operands and their
 // scales are in flight in registers at once (buffer loads; blocks past K and
 // rows past the operand's extent read as zeros).  Each block is written to one
-// of two LDS stages, one barrier per block, and consumed by a 2 x 2 grid of
-// v_mfma 16x16x128 per wave with the fragment conventions of the large-tile
-// kernel: the MFMA is issued with the B tile first, so lane l holds
-// C[m = l%16][n = 4*(l/16) .. +3] of each 16 x 16 sub-tile.
+// of two LDS stages, one barrier per block, and consumed by the wave's grid of
+// v_mfma 16x16x128 with the fragment conventions of the large-tile kernel: the
+// MFMA is issued with the B tile first, so lane l holds C[m = l%16][n =
+// 4*(l/16) .. +3] of each 16 x 16 sub-tile.
 //
 // Scaling granularities as in the large-tile kernel (gemm_fp8_kernel.py
 // :164-167, :524-528, :934-964 of the reference; MX with per-32-K E8M0
@@ -37,13 +37,22 @@ using gemm_detail::store4;
 using gemm_detail::v4f;
 using gemm_detail::v8i;
 
-constexpr int SBM = 64, SBN = 64, SBK = 128; // workgroup tile
-constexpr int SNTHR = 256;                   // four waves, 2 x 2 over the tile
-constexpr int SWT = 32;                      // wave tile 32 x 32 = 2 x 2 sub-tiles
-constexpr int ST = SWT / 16;
-constexpr int RING = 2;                      // K blocks in flight per thread (2, 4 and 8 measured: 2 is best)
-constexpr int STILE = SBM * SBK;             // one operand tile in LDS (8 KB)
-constexpr int SSTAGE = 2 * STILE;
+constexpr int SBK   = 128; // K block
+constexpr int SNTHR = 256; // four waves, 2 x 2 over the tile
+constexpr int RING  = 2;   // K blocks in flight per thread (2, 4 and 8 measured: 2 is best)
+
+// Workgroup tile shapes.  Per wave (SBM/2) x (SBN/2) of C = STM x STN MFMA
+// sub-tiles; per thread and K block, SBM/2 bytes of A and SBN/2 bytes of B.
+enum : int { TILE_32x64 = 0, TILE_64x64 = 1, TILE_128x128 = 2 };
+template <int TILE>
+struct STile {
+    static constexpr int BM  = TILE == TILE_128x128 ? 128 : (TILE == TILE_64x64 ? 64 : 32);
+    static constexpr int BN  = TILE == TILE_128x128 ? 128 : 64;
+    static constexpr int WTM = BM / 2, WTN = BN / 2;
+    static constexpr int STM = WTM / 16, STN = WTN / 16;
+    static constexpr int A_BYTES = BM * SBK, B_BYTES = BN * SBK;
+    static constexpr int STAGE   = A_BYTES + B_BYTES;
+};
 
 // Problem in the NT view: C[m, n] = sum_k A(m, k) B(n, k), with A(m, k) at
 // a[m * lda + k] (K-contiguous) or a[k * lda + m] (K-major), likewise B.
@@ -57,6 +66,7 @@ struct SmallArgs {
     // row r, 32-K block q at s[r * s_m + (q / 4) * s_k + q % 4]
     int64_t        sa_m, sa_k, sb_m, sb_k, sa_bytes, sb_bytes;
     int            a2d, b2d;
+    int            tile;    // TILE_* of this launch
     int            tiles_m, tiles_n;
     int            group_m; // tile rows per group of the tile order
     int            aligned_c;
@@ -66,7 +76,7 @@ struct SmallArgs {
 // eight 16-byte chunks, chunk c stored at position c ^ ((r ^ (r >> 3)) & 7).
 // The 16 rows of an MFMA fragment read see distinct chunk positions within
 // every 8 aligned rows, and the column writes of the K-major transpose (rows
-// 8 apart) land on distinct positions as well.
+// 4 to 16 apart) spread over the chunk positions as well.
 __device__ __forceinline__ int soff(int row, int ch) { return row * SBK + ((ch ^ ((row ^ (row >> 3)) & 7)) << 4); }
 
 // 32-bit offset that lies past any descriptor extent this kernel builds
@@ -83,65 +93,76 @@ __device__ __forceinline__ rsrc_t tile_rsrc(const uint8_t *p, int64_t bytes) {
                                              __builtin_amdgcn_readfirstlane(static_cast<int32_t>(bytes)), 0x00020000);
 }
 
-// Operand tile of 64 rows starting at row r0: base pointer and extent.  A
+// Operand tile of R rows starting at row r0: base pointer and extent.  A
 // K-contiguous tile ends after its last valid row's K bytes; a K-major tile
-// after the last K row's bytes up to the operand's row count rounded to 8 (the
-// 8-byte row loads stay whole; the host guarantees ld % 8 == 0 and rows <= ld).
-template <bool KM>
+// after the last K row's bytes up to the operand's row count rounded to 16
+// (the row loads of up to 16 bytes stay whole; the host guarantees
+// ld % 16 == 0 for a K-major operand, and rows <= ld).
+template <bool KM, int R>
 __device__ __forceinline__ rsrc_t operand_rsrc(const uint8_t *p, int64_t ld, int64_t r0, int64_t rows, int64_t K) {
     if constexpr (!KM) {
-        const int64_t valid = min<int64_t>(rows - r0, SBM);
+        const int64_t valid = min<int64_t>(rows - r0, R);
         return tile_rsrc(p + r0 * ld, (valid - 1) * ld + K);
     } else {
-        const int64_t end = min<int64_t>((rows + 7) & ~int64_t(7), ld);
+        const int64_t end = min<int64_t>((rows + 15) & ~int64_t(15), ld);
         return tile_rsrc(p + r0, (K - 1) * ld + end - r0);
     }
 }
 
-// One K block of an operand tile, 32 bytes per thread.
-//   K-contiguous: rows t/8 and t/8 + 32, 16-byte chunk t%8 of each.
-//   K-major: K rows k0 + 4(t/8) .. +3, tile rows 8(t%8) .. +7 of each.
-template <bool KM>
-__device__ __forceinline__ void load_operand(rsrc_t r, int ld, int k0, int K, uint32_t (&v)[8]) {
+// One K block of an R-row operand tile, R/2 bytes per thread.
+//   K-contiguous: rows t/8 + 32 q, 16-byte chunk t%8 of each.
+//   K-major: K rows k0 + 4(t/8) .. +3, tile rows (R/8)(t%8) .. +R/8-1 of each.
+template <bool KM, int R>
+__device__ __forceinline__ void load_operand(rsrc_t r, int ld, int k0, int K, uint32_t (&v)[R / 8]) {
     const int t = threadIdx.x;
     if constexpr (!KM) {
         const int c = t & 7, row = t >> 3;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < R / 32; ++q) {
             int off = (row + 32 * q) * ld + k0 + 16 * c;
             if (k0 + 16 * c >= K) off = OOB; // past K: zeros (not the next row's bytes)
             const uint4 x = gemm_detail::bload16(r, off, 0);
             v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
         }
     } else {
-        const int rg = t & 7, kg = t >> 3;
+        constexpr int W = R / 8; // bytes per K row and thread
+        const int     rg = t & 7, kg = t >> 3;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             // K rows past K start beyond the extent and read as zeros
-            const int off = (k0 + 4 * kg + j) * ld + 8 * rg;
-            const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-            v[2 * j] = x.x; v[2 * j + 1] = x.y;
+            const int off = (k0 + 4 * kg + j) * ld + W * rg;
+            if constexpr (W == 4) {
+                v[j] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+            } else if constexpr (W == 8) {
+                const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+                v[2 * j] = x.x; v[2 * j + 1] = x.y;
+            } else {
+                const uint4 x = gemm_detail::bload16(r, off, 0);
+                v[4 * j] = x.x; v[4 * j + 1] = x.y; v[4 * j + 2] = x.z; v[4 * j + 3] = x.w;
+            }
         }
     }
 }
 
 // Store one K block of an operand tile into LDS at T (see soff for the layout).
-template <bool KM>
-__device__ __forceinline__ void write_operand(uint8_t *T, const uint32_t (&v)[8]) {
+template <bool KM, int R>
+__device__ __forceinline__ void write_operand(uint8_t *T, const uint32_t (&v)[R / 8]) {
     const int t = threadIdx.x;
     if constexpr (!KM) {
         const int c = t & 7, row = t >> 3;
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+        for (int q = 0; q < R / 32; ++q)
             *reinterpret_cast<uint4 *>(T + soff(row + 32 * q, c)) = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
     } else {
-        // v[2j + h] holds K row kk + j, tile rows 8 rg + 4h .. +3 (one byte each);
-        // transpose each 4 x 4 byte block so that a dword holds K kk .. kk+3 of one row
-        const int rg = t & 7, kk = 4 * (t >> 3);
-        const int ch = kk >> 4, w = kk & 15;
+        // v[j * H + h] holds K row kk + j, tile rows W rg + 4h .. +3 (one byte
+        // each); transpose each 4 x 4 byte block so that a dword holds K
+        // kk .. kk+3 of one row
+        constexpr int W = R / 8, H = W / 4;
+        const int     rg = t & 7, kk = 4 * (t >> 3);
+        const int     ch = kk >> 4, w = kk & 15;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t a = v[h], b = v[2 + h], c = v[4 + h], d = v[6 + h];
+        for (int h = 0; h < H; ++h) {
+            const uint32_t a = v[h], b = v[H + h], c = v[2 * H + h], d = v[3 * H + h];
             const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u); // a0 b0 a1 b1
             const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u); // a2 b2 a3 b3
             const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);
@@ -152,22 +173,25 @@ __device__ __forceinline__ void write_operand(uint8_t *T, const uint32_t (&v)[8]
                                      __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u)};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<uint32_t *>(T + soff(8 * rg + 4 * h + i, ch) + w) = col[i];
+                *reinterpret_cast<uint32_t *>(T + soff(W * rg + 4 * h + i, ch) + w) = col[i];
         }
     }
 }
 
 // Registers of one in-flight K block.
+template <class TL>
 struct Slot {
-    uint32_t a[8], b[8];
-    float    sa[ST];      // BLOCKWISE: A scale of the lane's row in sub-tile i
-    float    sb[ST][4];   // BLOCKWISE: B scales of the lane's four columns in sub-tile j
-    int      ea[ST], eb[ST]; // MX: exponent bytes of the lane's A / B rows
+    uint32_t a[TL::BM / 8], b[TL::BN / 8];
+    float    sa[TL::STM];      // BLOCKWISE: A scale of the lane's row in sub-tile i
+    float    sb[TL::STN][4];   // BLOCKWISE: B scales of the lane's four columns in sub-tile j
+    int      ea[TL::STM], eb[TL::STN]; // MX: exponent bytes of the lane's A / B rows
 };
 
-template <int SM, int FA, int FB, int OUT_DT, bool AKM, bool BKM>
+template <int SM, int FA, int FB, int OUT_DT, bool AKM, bool BKM, int TILE>
 __global__ __launch_bounds__(SNTHR) void gemm_small_kernel(const SmallArgs g) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * SSTAGE];
+    using TL = STile<TILE>;
+    constexpr int SBM = TL::BM, SBN = TL::BN, WTM = TL::WTM, WTN = TL::WTN, STM = TL::STM, STN = TL::STN;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * TL::STAGE];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int fr = lane & 15, fg = lane >> 4;
@@ -189,89 +213,96 @@ __global__ __launch_bounds__(SNTHR) void gemm_small_kernel(const SmallArgs g) {
     const int     nk = static_cast<int>((K + SBK - 1) / SBK);
     const int     Ki = static_cast<int>(K);
 
-    const rsrc_t rA = operand_rsrc<AKM>(g.a, g.lda, m0, M, K);
-    const rsrc_t rB = operand_rsrc<BKM>(g.b, g.ldb, n0, N, K);
+    const rsrc_t rA = operand_rsrc<AKM, SBM>(g.a, g.lda, m0, M, K);
+    const rsrc_t rB = operand_rsrc<BKM, SBN>(g.b, g.ldb, n0, N, K);
     const int    lda = static_cast<int>(g.lda), ldb = static_cast<int>(g.ldb);
 
     // scale addressing: the lane's rows m (one per A sub-tile) and columns n
     // (four per B sub-tile), clamped into the operand so every read is in range
     const rsrc_t rSA = tile_rsrc(static_cast<const uint8_t *>(g.sa), g.sa_bytes);
     const rsrc_t rSB = tile_rsrc(static_cast<const uint8_t *>(g.sb), g.sb_bytes);
-    int          sa_vo[ST], sb_vo[ST][4];
+    int          sa_vo[STM], sb_vo[STN][4];
 #pragma unroll
-    for (int i = 0; i < ST; ++i) {
-        const int64_t m = min<int64_t>(m0 + wm * SWT + 16 * i + fr, M - 1);
-        const int64_t n = min<int64_t>(n0 + wn * SWT + 16 * i + fr, N - 1);
+    for (int i = 0; i < STM; ++i) {
+        const int64_t m = min<int64_t>(m0 + wm * WTM + 16 * i + fr, M - 1);
+        if constexpr (SM == SM_BLOCK) sa_vo[i] = static_cast<int>((g.a2d ? (m >> 7) : m) * g.sa_m) * 4;
+        else if constexpr (SM == SM_MX) sa_vo[i] = static_cast<int>(m * g.sa_m) + fg;
+    }
+#pragma unroll
+    for (int j = 0; j < STN; ++j) {
         if constexpr (SM == SM_BLOCK) {
-            sa_vo[i] = static_cast<int>((g.a2d ? (m >> 7) : m) * g.sa_m) * 4;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t nc = min<int64_t>(n0 + wn * SWT + 16 * i + 4 * fg + r, N - 1);
-                sb_vo[i][r] = static_cast<int>((g.b2d ? (nc >> 7) : nc) * g.sb_m) * 4;
+                const int64_t nc = min<int64_t>(n0 + wn * WTN + 16 * j + 4 * fg + r, N - 1);
+                sb_vo[j][r] = static_cast<int>((g.b2d ? (nc >> 7) : nc) * g.sb_m) * 4;
             }
         } else if constexpr (SM == SM_MX) {
-            sa_vo[i] = static_cast<int>(m * g.sa_m) + fg;
-            sb_vo[i][0] = static_cast<int>(n * g.sb_m) + fg;
+            const int64_t n = min<int64_t>(n0 + wn * WTN + 16 * j + fr, N - 1);
+            sb_vo[j][0] = static_cast<int>(n * g.sb_m) + fg;
         }
     }
 
-    auto load_slot = [&](int kb, Slot &s) {
+    auto load_slot = [&](int kb, Slot<TL> &s) {
         const int k0 = kb * SBK;
-        load_operand<AKM>(rA, lda, k0, Ki, s.a);
-        load_operand<BKM>(rB, ldb, k0, Ki, s.b);
+        load_operand<AKM, SBM>(rA, lda, k0, Ki, s.a);
+        load_operand<BKM, SBN>(rB, ldb, k0, Ki, s.b);
         if constexpr (SM == SM_BLOCK) {
             const int ka = static_cast<int>(kb * g.sa_k) * 4, kbb = static_cast<int>(kb * g.sb_k) * 4;
 #pragma unroll
-            for (int i = 0; i < ST; ++i) {
-                s.sa[i] = gemm_detail::bload_f32(rSA, sa_vo[i], ka);
+            for (int i = 0; i < STM; ++i) s.sa[i] = gemm_detail::bload_f32(rSA, sa_vo[i], ka);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) s.sb[i][r] = gemm_detail::bload_f32(rSB, sb_vo[i][r], kbb);
-            }
+            for (int j = 0; j < STN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s.sb[j][r] = gemm_detail::bload_f32(rSB, sb_vo[j][r], kbb);
         } else if constexpr (SM == SM_MX) {
             const int ka = static_cast<int>(kb * g.sa_k), kbb = static_cast<int>(kb * g.sb_k);
 #pragma unroll
-            for (int i = 0; i < ST; ++i) {
-                s.ea[i] = gemm_detail::bload_u8(rSA, sa_vo[i], ka);
-                s.eb[i] = gemm_detail::bload_u8(rSB, sb_vo[i][0], kbb);
-            }
+            for (int i = 0; i < STM; ++i) s.ea[i] = gemm_detail::bload_u8(rSA, sa_vo[i], ka);
+#pragma unroll
+            for (int j = 0; j < STN; ++j) s.eb[j] = gemm_detail::bload_u8(rSB, sb_vo[j][0], kbb);
         }
     };
 
-    // fragment offsets: rows wm*32 + 16 i + fr of A, wn*32 + 16 j + fr of B
-    int aoff[ST][2], boff[ST][2];
+    // fragment offsets: rows wm*WTM + 16 i + fr of A, wn*WTN + 16 j + fr of B
+    int aoff[STM][2], boff[STN][2];
 #pragma unroll
-    for (int i = 0; i < ST; ++i) {
-        aoff[i][0] = soff(wm * SWT + 16 * i + fr, fg);
-        aoff[i][1] = soff(wm * SWT + 16 * i + fr, 4 + fg);
-        boff[i][0] = STILE + soff(wn * SWT + 16 * i + fr, fg);
-        boff[i][1] = STILE + soff(wn * SWT + 16 * i + fr, 4 + fg);
+    for (int i = 0; i < STM; ++i) {
+        aoff[i][0] = soff(wm * WTM + 16 * i + fr, fg);
+        aoff[i][1] = soff(wm * WTM + 16 * i + fr, 4 + fg);
+    }
+#pragma unroll
+    for (int j = 0; j < STN; ++j) {
+        boff[j][0] = TL::A_BYTES + soff(wn * WTN + 16 * j + fr, fg);
+        boff[j][1] = TL::A_BYTES + soff(wn * WTN + 16 * j + fr, 4 + fg);
     }
 
-    v4f acc[ST][ST];
+    v4f acc[STN][STM];
 #pragma unroll
-    for (int j = 0; j < ST; ++j)
+    for (int j = 0; j < STN; ++j)
 #pragma unroll
-        for (int i = 0; i < ST; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < STM; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
 
     // Epilogue scales, read now: issued ahead of the operand loads, they are
     // long in registers when the epilogue needs them (a read there would cost
     // one more memory round trip).  Volatile: kept here, not sunk past the loop.
     constexpr int VOL = static_cast<int>(1u << 31);
-    float ts = 1.0f, ra[ST] = {}, rb[ST][4] = {};
+    float ts = 1.0f, ra[STM] = {}, rb[STN][4] = {};
     if constexpr (SM == SM_TENSOR) {
         ts = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSA, 0, 0, VOL)) *
              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSB, 0, 0, VOL));
     } else if constexpr (SM == SM_ROW) {
 #pragma unroll
-        for (int i = 0; i < ST; ++i) {
-            const int m = static_cast<int>(min<int64_t>(m0 + wm * SWT + 16 * i + fr, M - 1));
+        for (int i = 0; i < STM; ++i) {
+            const int m = static_cast<int>(min<int64_t>(m0 + wm * WTM + 16 * i + fr, M - 1));
             ra[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSA, 4 * m, 0, VOL));
+        }
+#pragma unroll
+        for (int j = 0; j < STN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int n = static_cast<int>(min<int64_t>(n0 + wn * SWT + 16 * i + 4 * fg + r, N - 1));
-                rb[i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSB, 4 * n, 0, VOL));
+                const int n = static_cast<int>(min<int64_t>(n0 + wn * WTN + 16 * j + 4 * fg + r, N - 1));
+                rb[j][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSB, 4 * n, 0, VOL));
             }
-        }
     }
 
     // Block kb is consumed in iteration kb: its fragments are read from LDS
@@ -286,10 +317,10 @@ __global__ __launch_bounds__(SNTHR) void gemm_small_kernel(const SmallArgs g) {
     // slot's loads and their use.  Its first pass (kb0 = -RING) fills the ring
     // and writes block 0: the slots keep one set of registers throughout, with
     // no peeled prologue whose register copies would wait for loads in flight.
-    Slot ring[RING];
-    float sa[ST] = {}, sb[ST][4] = {}; // scales of the block being consumed
-    int   ea[ST] = {}, eb[ST] = {};
-    int   kb_first = -RING;
+    Slot<TL> ring[RING];
+    float    sa[STM] = {}, sb[STN][4] = {}; // scales of the block being consumed
+    int      ea[STM] = {}, eb[STN] = {};
+    int      kb_first = -RING;
     asm volatile("" : "+s"(kb_first)); // opaque start: not peeled
     for (int kb0 = kb_first; kb0 < nk; kb0 += RING) {
 #pragma unroll
@@ -298,59 +329,62 @@ __global__ __launch_bounds__(SNTHR) void gemm_small_kernel(const SmallArgs g) {
             const int  sn    = (s + 1) % RING;
             const bool live  = kb >= 0 && kb < nk;
             const bool wlive = kb >= -1 && kb + 1 < nk;
-            const uint8_t *S = smem + (s & 1) * SSTAGE;
-            uint8_t       *W = smem + ((s + 1) & 1) * SSTAGE;
-            v8i af[ST], bf[ST];
+            const uint8_t *S = smem + (s & 1) * TL::STAGE;
+            uint8_t       *W = smem + ((s + 1) & 1) * TL::STAGE;
+            v8i af[STM];
             if (live) {
 #pragma unroll
-                for (int i = 0; i < ST; ++i) {
-                    af[i] = frag(S, aoff[i][0], aoff[i][1]);
-                    bf[i] = frag(S, boff[i][0], boff[i][1]);
-                }
+                for (int i = 0; i < STM; ++i) af[i] = frag(S, aoff[i][0], aoff[i][1]);
             }
             // scales of block kb leave slot s before it is refilled
-            float csa[ST], csb[ST][4];
-            int   cea[ST], ceb[ST];
+            float csa[STM], csb[STN][4];
+            int   cea[STM], ceb[STN];
 #pragma unroll
-            for (int i = 0; i < ST; ++i) {
-                csa[i] = sa[i]; cea[i] = ea[i]; ceb[i] = eb[i];
+            for (int i = 0; i < STM; ++i) { csa[i] = sa[i]; cea[i] = ea[i]; }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) csb[i][r] = sb[i][r];
+            for (int j = 0; j < STN; ++j) {
+                ceb[j] = eb[j];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) csb[j][r] = sb[j][r];
             }
             if (wlive) {
-                write_operand<AKM>(W, ring[sn].a);
-                write_operand<BKM>(W + STILE, ring[sn].b);
+                write_operand<AKM, SBM>(W, ring[sn].a);
+                write_operand<BKM, SBN>(W + TL::A_BYTES, ring[sn].b);
+                if constexpr (SM == SM_BLOCK) {
 #pragma unroll
-                for (int i = 0; i < ST; ++i) {
-                    if constexpr (SM == SM_BLOCK) {
-                        sa[i] = ring[sn].sa[i];
+                    for (int i = 0; i < STM; ++i) sa[i] = ring[sn].sa[i];
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) sb[i][r] = ring[sn].sb[i][r];
-                    } else if constexpr (SM == SM_MX) {
-                        ea[i] = ring[sn].ea[i];
-                        eb[i] = ring[sn].eb[i];
-                    }
+                    for (int j = 0; j < STN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sb[j][r] = ring[sn].sb[j][r];
+                } else if constexpr (SM == SM_MX) {
+#pragma unroll
+                    for (int i = 0; i < STM; ++i) ea[i] = ring[sn].ea[i];
+#pragma unroll
+                    for (int j = 0; j < STN; ++j) eb[j] = ring[sn].eb[j];
                 }
             }
             load_slot(kb + RING, ring[s]);
             if (live) {
 #pragma unroll
-                for (int j = 0; j < ST; ++j)
+                for (int j = 0; j < STN; ++j) {
+                    const v8i bf = frag(S, boff[j][0], boff[j][1]);
 #pragma unroll
-                    for (int i = 0; i < ST; ++i) {
+                    for (int i = 0; i < STM; ++i) {
                         if constexpr (SM == SM_BLOCK) {
                             const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                                bf[j], af[i], v4f{0.f, 0.f, 0.f, 0.f}, FB, FA, 0, 0, 0, 0);
+                                bf, af[i], v4f{0.f, 0.f, 0.f, 0.f}, FB, FA, 0, 0, 0, 0);
 #pragma unroll
                             for (int r = 0; r < 4; ++r) acc[j][i][r] += p[r] * (csa[i] * csb[j][r]);
                         } else if constexpr (SM == SM_MX) {
                             acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                                bf[j], af[i], acc[j][i], FB, FA, 0, ceb[j], 0, cea[i]);
+                                bf, af[i], acc[j][i], FB, FA, 0, ceb[j], 0, cea[i]);
                         } else {
                             acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                                bf[j], af[i], acc[j][i], FB, FA, 0, 0, 0, 0);
+                                bf, af[i], acc[j][i], FB, FA, 0, 0, 0, 0);
                         }
                     }
+                }
             }
             if (wlive) __syncthreads();
         }
@@ -358,11 +392,11 @@ __global__ __launch_bounds__(SNTHR) void gemm_small_kernel(const SmallArgs g) {
 
     // ---- epilogue: scale and store, 4 consecutive n per lane and sub-tile ----
 #pragma unroll
-    for (int j = 0; j < ST; ++j) {
-        const int64_t n = n0 + wn * SWT + 16 * j + 4 * fg;
+    for (int j = 0; j < STN; ++j) {
+        const int64_t n = n0 + wn * WTN + 16 * j + 4 * fg;
 #pragma unroll
-        for (int i = 0; i < ST; ++i) {
-            const int64_t m = m0 + wm * SWT + 16 * i + fr;
+        for (int i = 0; i < STM; ++i) {
+            const int64_t m = m0 + wm * WTM + 16 * i + fr;
             if (m >= M || n >= N) continue;
             float x[4];
 #pragma unroll
@@ -381,7 +415,11 @@ __global__ __launch_bounds__(SNTHR) void gemm_small_kernel(const SmallArgs g) {
 template <int SM, bool AKM, bool BKM, int FA, int FB, int OUT_DT>
 int launch_small(const SmallArgs &g, hipStream_t st) {
     const uint32_t grid = static_cast<uint32_t>(g.tiles_m) * static_cast<uint32_t>(g.tiles_n);
-    gemm_small_kernel<SM, FA, FB, OUT_DT, AKM, BKM><<<grid, SNTHR, 0, st>>>(g);
+    switch (g.tile) {
+    case TILE_32x64: gemm_small_kernel<SM, FA, FB, OUT_DT, AKM, BKM, TILE_32x64><<<grid, SNTHR, 0, st>>>(g); break;
+    case TILE_64x64: gemm_small_kernel<SM, FA, FB, OUT_DT, AKM, BKM, TILE_64x64><<<grid, SNTHR, 0, st>>>(g); break;
+    default: gemm_small_kernel<SM, FA, FB, OUT_DT, AKM, BKM, TILE_128x128><<<grid, SNTHR, 0, st>>>(g); break;
+    }
     PTA_CHECK_LAUNCH();
     return PTA_OK;
 }

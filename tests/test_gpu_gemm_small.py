@@ -97,7 +97,10 @@ def _case(M, N, K, layout, trans_c, gran_name, fa=E4, fb=E4, out_dtype=torch.bfl
     assert not bool(diff.any()), f"{int(diff.sum())} of {diff.numel()} outputs differ, first at {diff.nonzero()[0].tolist()}"
 
 
-SHAPES = [(512, 1024, 1024), (255, 512, 576), (64, 128, 128), (200, 136, 1040), (8, 24, 16), (1000, 520, 2048)]
+# 32 x 64 tiles for the first six, 64 x 64 for (1024, 1024) and (1000, 1040),
+# 128 x 128 for (1904, 2000) (ragged in both dimensions)
+SHAPES = [(512, 1024, 1024), (255, 512, 576), (64, 128, 128), (200, 136, 1040), (8, 24, 16), (1000, 520, 2048),
+          (1024, 1024, 256), (1000, 1040, 384), (1904, 2000, 256)]
 
 
 @pytest.mark.parametrize("mnk", SHAPES)
@@ -111,7 +114,8 @@ def test_small_path_matches_large_tile_kernel(mnk, layout, trans_c, gran):
     _case(M, N, K, layout, trans_c, gran)
 
 
-@pytest.mark.parametrize("mnk", [(512, 1024, 1024), (255, 512, 640), (64, 128, 128), (200, 136, 1024)])
+@pytest.mark.parametrize("mnk", [(512, 1024, 1024), (255, 512, 640), (64, 128, 128), (200, 136, 1024),
+                                 (1000, 1040, 512), (1904, 2000, 256)])
 @pytest.mark.parametrize("trans_c", [False, True])
 def test_small_path_mx_matches_large_tile_kernel(mnk, trans_c):
     M, N, K = mnk
@@ -121,6 +125,7 @@ def test_small_path_mx_matches_large_tile_kernel(mnk, trans_c):
 @pytest.mark.parametrize("fmts", [(E4, E5), (E5, E4), (E5, E5)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("gran", ["TENSORWISE", "BLOCKWISE", "MX_BLOCKWISE"])
-def test_small_path_formats_and_outputs(fmts, out_dtype, gran):
+@pytest.mark.parametrize("mnk", [(320, 200, 384), (1904, 2000, 256)])
+def test_small_path_formats_and_outputs(fmts, out_dtype, gran, mnk):
     layout = "NT" if gran == "MX_BLOCKWISE" else "NN"
-    _case(320, 200, 384, layout, False, gran, fmts[0], fmts[1], out_dtype)
+    _case(*mnk, layout, False, gran, fmts[0], fmts[1], out_dtype)
