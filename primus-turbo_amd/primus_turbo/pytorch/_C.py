@@ -124,17 +124,34 @@ def load():
     return _lib
 
 
+_fns: dict = {}
+_queries: dict = {}
+
+
+def _fn(name: str):
+    f = _fns.get(name)
+    if f is None:
+        f = _fns[name] = getattr(load(), name)
+    return f
+
+
 def call(name: str, *args) -> None:
     """Call a status-returning entry point and raise RuntimeError on failure."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    rc = _fn(name)(*args)
     if rc != 0:
-        msg = lib.pta_last_error().decode("utf-8", "replace")
+        msg = load().pta_last_error().decode("utf-8", "replace")
         raise RuntimeError(f"{name} failed ({rc}): {msg}")
 
 
 def query(name: str, *args) -> int:
-    return int(getattr(load(), name)(*args))
+    """A size query (a pure function of its integer arguments; answers are cached)."""
+    key = (name, args)
+    v = _queries.get(key)
+    if v is None:
+        if len(_queries) >= 4096:  # shapes that vary per call (token counts) must not grow it forever
+            _queries.clear()
+        v = _queries[key] = int(_fn(name)(*args))
+    return v
 
 
 def ptr(t) -> int | None:
@@ -144,9 +161,22 @@ def ptr(t) -> int | None:
     return t.data_ptr()
 
 
+_gpu_checked = False
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device=None) -> int:
-    if not torch.cuda.is_available():
-        raise RuntimeError("primus_turbo FP8 ops need a ROCm GPU (torch.cuda.is_available() is False)")
+    """Handle of torch's current stream on `device` (the stream every entry is launched on)."""
+    global _gpu_checked
+    if not _gpu_checked:
+        if not torch.cuda.is_available():
+            raise RuntimeError("primus_turbo FP8 ops need a ROCm GPU (torch.cuda.is_available() is False)")
+        _gpu_checked = True
+    if _raw_stream is not None:
+        if device is not None and not isinstance(device, (torch.device, int)):
+            device = torch.device(device)
+        idx = device.index if isinstance(device, torch.device) else device
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

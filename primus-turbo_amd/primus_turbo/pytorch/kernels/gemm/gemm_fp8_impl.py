@@ -35,6 +35,8 @@ def _gran_code(granularity) -> int:
 def _scale_arg(s: torch.Tensor, gran: int) -> torch.Tensor:
     if gran == ScalingGranularity.MX_BLOCKWISE.value:
         return s.contiguous().view(torch.uint8)
+    if s.dtype == torch.float32 and s.is_contiguous():
+        return s
     return s.contiguous().to(torch.float32)
 
 
