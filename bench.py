@@ -58,6 +58,22 @@ def _time_cuda(fn, steps: int, warmup: int):
     return start.elapsed_time(end) / steps  # ms per call (events on the launch stream)
 
 
+def _per_call_ms(fn, n: int):
+    """Median and p10 / p90 of n calls, each bracketed by its own HIP events
+    on the launch stream (a distribution next to the bracketed average)."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for s, e in evs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    t = sorted(s.elapsed_time(e) for s, e in evs)
+    q = lambda f: t[min(n - 1, int(f * (n - 1) + 0.5))]  # noqa: E731
+    return {"n": n, "p10": round(q(0.1), 4), "median": round(q(0.5), 4), "p90": round(q(0.9), 4)}
+
+
 def _time_settled(fn, steps: int, settle_ms: float = 40.0):
     """_time_cuda after _settle: each extra measurement first runs its call
     until settle_ms of GPU time has passed."""
@@ -264,6 +280,7 @@ def main():
     ms = _time_cuda(gemm, args.steps, args.warmup)
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
+    per_call = _per_call_ms(gemm, 100)  # distribution, after (outside) the timed region
 
     extras = {}
     if args.only == "quant":
@@ -302,6 +319,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
         "settle_ms": round(settle_ms, 1),
+        "per_call_ms": per_call,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
