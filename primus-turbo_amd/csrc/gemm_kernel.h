@@ -349,23 +349,35 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
     const int mx_vo = wave < 4 ? static_cast<int>((m0 + 64 * wave + lane) * g.sa_m)
                                : static_cast<int>((n0 + 64 * (wave - 4) + lane) * g.sb_m);
     const int mx_ks = static_cast<int>(wave < 4 ? g.sa_k : g.sb_k); // exponent bytes per K block
+    // Operand DMAs are issued by waves 0 .. NWAVES/2-1 only, each for its own
+    // rows and those of wave + NWAVES/2 (the other wave on its SIMD, as waves
+    // go round-robin over the 4 SIMDs).  The non-issuing wave of each SIMD
+    // starts its MFMAs right after its fragment reads and keeps the matrix
+    // pipe busy while its partner issues (3% faster than every wave issuing
+    // its own rows at the headline shape).
+    constexpr int HALF = NWAVES / 2;
+    const bool    dma_wave = __builtin_amdgcn_readfirstlane(wave) < HALF;
+    const int     pA = HALF * RPW_A * static_cast<int>(g.lda), pB = HALF * RPW_B * static_cast<int>(g.ldb);
     auto issue = [&](int kb, int stage) {
         const int      k0 = kb * BK;
         const uint32_t la = lds0 + stage * STAGE_ + wave * RPW_A * BK;
         const uint32_t lb = lds0 + stage * STAGE_ + TILE_A_BYTES + wave * RPW_B * BK;
-        // chunks past K (last block only) read out of range and land as zeros
+        // chunks past K (last block only) read out of range and land as zeros;
+        // the row offset stays in the per-lane offset so partial tiles are
+        // range-checked by the descriptor
         const bool last = ktail && kb + 1 == nk;
+        const bool oob  = last && k0 + 16 * ch >= K;
+        if (dma_wave) {
 #pragma unroll
-        for (int d = 0; d < DA; ++d) {
-            int v = vA[d];
-            if (last && k0 + 16 * ch >= K) v = 0x7fffffff - 64;
-            dma16(la + d * 8 * BK, v, dA, k0);
-        }
+            for (int d = 0; d < DA; ++d) {
+                dma16(la + d * 8 * BK, oob ? 0x7fffffff - 64 : vA[d], dA, k0);
+                dma16(la + HALF * RPW_A * BK + d * 8 * BK, oob ? 0x7fffffff - 64 : vA[d] + pA, dA, k0);
+            }
 #pragma unroll
-        for (int d = 0; d < DB; ++d) {
-            int v = vB[d];
-            if (last && k0 + 16 * ch >= K) v = 0x7fffffff - 64;
-            dma16(lb + d * 8 * BK, v, dB, k0);
+            for (int d = 0; d < DB; ++d) {
+                dma16(lb + d * 8 * BK, oob ? 0x7fffffff - 64 : vB[d], dB, k0);
+                dma16(lb + HALF * RPW_B * BK + d * 8 * BK, oob ? 0x7fffffff - 64 : vB[d] + pB, dB, k0);
+            }
         }
         if constexpr (SM == SM_BLOCK && !B2D) {
             // waves 0..3 each stage 64 column scales of this K block
@@ -447,10 +459,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
 
     for (int kb = 0; kb < nk; ++kb) {
         const int cur = kb & 1;
-        if (kb + 1 < nk) {
-            load_scales(kb + 1, sc_nxt);
-            issue(kb + 1, cur ^ 1);
-        }
+        if (kb + 1 < nk) load_scales(kb + 1, sc_nxt);
         const uint8_t *S = smem + cur * STAGE_;
         v8i            af[TM];
 #pragma unroll
@@ -461,6 +470,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
             for (int i = 0; i < TM; ++i) s_i[i] = sc_cur.sa[i] * sc_cur.sb_u;
         }
         v8i bf = frag(S, boff0, boff1);
+        // the next stage's DMAs go out behind this step's first fragment reads
+        // (stage cur ^ 1 was last read before the previous step's barrier)
+        if (kb + 1 < nk) issue(kb + 1, cur ^ 1);
         const float *SBL = reinterpret_cast<const float *>(smem + SBASE_ + cur * SSLOT_) + wn * WTN_ + 4 * fg;
         int ea[TM], eb[TN_];
         if constexpr (SM == SM_MX) {
