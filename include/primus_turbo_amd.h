@@ -64,7 +64,10 @@ size_t pta_quantize_fp8_tensorwise_workspace_size(int64_t n);
 
 /* Tensorwise: amax = max|x| (NaN ignored), scale = fp8_max / max(amax, 1e-12),
  * q = fp8(clamp(x * scale)), *scale_inv = 1 / scale.  If scale is non-NULL it
- * is a device scalar used instead of the amax-derived one.
+ * is a device scalar used instead of the amax-derived one.  Up to 2^21
+ * elements (16-byte aligned x and q, stream not capturing) this is one launch
+ * whose workgroups exchange partial maxima through the workspace; if that
+ * exchange does not complete, *scale_inv is NaN.  Otherwise two launches. */
  * Replaces quantize_fp8_tensorwise (csrc/pytorch/quantization/quantization.cpp:42-88). */
 int pta_quantize_fp8_tensorwise(const void *x, int in_dtype, int64_t n, const float *scale,
                                 void *q, int fmt, float *scale_inv, void *workspace,

@@ -14,6 +14,10 @@
 //   e8m0 = clamp(E + 127, 0, 254), q = fp8(x * 2^(127 - e8m0)).
 #include "common.h"
 
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
 #include <mutex>
 
 namespace pta {
@@ -99,6 +103,123 @@ int tw_grid(int64_t n) {
     if (g < 1) g = 1;
     if (g > TW_MAX_PARTS) g = TW_MAX_PARTS;
     return static_cast<int>(g);
+}
+
+// One launch for tensors of up to TW_FUSED_MAX elements: each thread keeps its
+// IT x 16 elements in registers, the workgroups publish their partial amax,
+// wait until every workgroup has published, reduce all partials and cast from
+// the registers: one read of x instead of two, one launch instead of two.
+// Publication: partial[b], then, once that store has completed, tag[b] = this
+// call's 64-bit tag, both device-coherent; thread i of every workgroup polls
+// tag[i] with device-coherent loads and then reads partial[i] the same way.
+// The tag is unique per call, so a workspace that holds an earlier call's tags
+// needs no clearing, and calls on different streams use their own workspaces.
+// At most TW_FUSED_GRID workgroups of 256 threads and little LDS: they are all
+// resident together on the 256 CUs.  A poll that has not seen every tag after
+// TW_SPIN_LIMIT rounds gives up and the call's scale becomes NaN, so a failure
+// shows in the output instead of hanging.  A tag fixed at graph capture would
+// repeat on every replay, so captured calls use the two-launch form.
+constexpr int      TW_FUSED_GRID = 128; // workgroups at most (<= NT: one partial per thread;
+                                        // 256 measured slower than the two-launch form)
+constexpr int64_t  TW_FUSED_MAX  = int64_t(TW_FUSED_GRID) * NT * 16 * 4;
+constexpr unsigned TW_SPIN_LIMIT = 1u << 22;
+constexpr size_t   TW_TAG_OFFSET = TW_FUSED_GRID * sizeof(float); // tags after the partials
+static_assert(TW_TAG_OFFSET + TW_FUSED_GRID * sizeof(uint64_t) <= TW_MAX_PARTS * sizeof(float),
+              "partials and tags fit the tensorwise workspace");
+
+template <int IN_DT, int FMT, int IT>
+__global__ __launch_bounds__(NT) void tw_fused_kernel(const void *x, int64_t n, uint8_t *q, float *scale_inv,
+                                                      float *partial, uint64_t *tags, uint64_t tag) {
+    const int     tid    = static_cast<int>(threadIdx.x);
+    const int     b      = static_cast<int>(blockIdx.x);
+    const int     g      = static_cast<int>(gridDim.x);
+    const int64_t stride = static_cast<int64_t>(g) * NT * 16;
+    const int64_t base0  = (static_cast<int64_t>(b) * NT + tid) * 16;
+    float         v[IT][16];
+    float         a = 0.0f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int64_t base = base0 + it * stride;
+        if (base + 16 <= n) {
+            float lo[8], hi[8];
+            load8<IN_DT>(x, base, lo);
+            load8<IN_DT>(x, base + 8, hi);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) { v[it][j] = lo[j]; v[it][j + 8] = hi[j]; }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[it][j] = base + j < n ? load_scalar<IN_DT>(x, base + j) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[it][j]));
+    }
+    __shared__ float s[NT / 64];
+    a = max64(a);
+    if ((tid & 63) == 0) s[tid >> 6] = a;
+    __syncthreads();
+    if (tid == 0) {
+        // device-coherent stores; the tag goes out once the partial's store
+        // has completed (no release fence: that would write back all of L2)
+        __hip_atomic_store(&partial[b], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __hip_atomic_store(&tags[b], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float pa   = 0.0f;
+    bool  seen = true;
+    if (tid < g) {
+        unsigned k = 0;
+        // device-coherent polls; the partial is read (device-coherent) only
+        // after its tag has been seen
+        while (__hip_atomic_load(&tags[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag && k < TW_SPIN_LIMIT) {
+            ++k;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        asm volatile("" ::: "memory");
+        seen = k < TW_SPIN_LIMIT;
+        pa   = __hip_atomic_load(&partial[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const bool all_seen = __syncthreads_and(seen);
+    pa = max64(pa);
+    if ((tid & 63) == 0) s[tid >> 6] = pa; // s[] free again: every read of it precedes __syncthreads_and
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    const float sc   = all_seen ? scale_from_amax<FMT>(amax, 1e-12f) : __builtin_nanf("");
+    if (b == 0 && tid == 0) scale_inv[0] = 1.0f / sc;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int64_t base = base0 + it * stride;
+        if (base + 16 <= n) {
+            *reinterpret_cast<uint4 *>(q + base) = make_uint4(quant4<FMT>(v[it], sc), quant4<FMT>(v[it] + 4, sc),
+                                                              quant4<FMT>(v[it] + 8, sc), quant4<FMT>(v[it] + 12, sc));
+        } else {
+            for (int j = 0; j < 16; ++j)
+                if (base + j < n) q[base + j] = cvt1_fp8<FMT>(qclamp<FMT>(v[it][j], sc));
+        }
+    }
+}
+
+// per-call tags: a per-process salt (process id, start time) xor a counter
+uint64_t tw_next_tag() {
+    static std::atomic<uint64_t> ctr{0};
+    static const uint64_t        salt =
+        (static_cast<uint64_t>(getpid()) << 40) ^
+        (static_cast<uint64_t>(std::chrono::steady_clock::now().time_since_epoch().count()) << 16);
+    return salt ^ (ctr.fetch_add(1, std::memory_order_relaxed) + 1);
+}
+
+template <int IN_DT, int FMT>
+int tw_fused_launch(const void *x, int64_t n, uint8_t *q, float *scale_inv, float *parts, hipStream_t st) {
+    const int64_t per  = static_cast<int64_t>(NT) * 16;
+    const int     it   = n <= per * TW_FUSED_GRID ? 1 : n <= 2 * per * TW_FUSED_GRID ? 2 : 4;
+    const int     g    = static_cast<int>(std::max<int64_t>(1, cdiv(n, per * it)));
+    uint64_t     *tags = reinterpret_cast<uint64_t *>(reinterpret_cast<uint8_t *>(parts) + TW_TAG_OFFSET);
+    const uint64_t tag = tw_next_tag();
+    if (it == 1) tw_fused_kernel<IN_DT, FMT, 1><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
+    else if (it == 2) tw_fused_kernel<IN_DT, FMT, 2><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
+    else tw_fused_kernel<IN_DT, FMT, 4><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
+    PTA_CHECK_LAUNCH();
+    return PTA_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -581,6 +702,13 @@ __global__ __launch_bounds__(NT) void transpose_u8_kernel(const uint8_t *x, int6
 template <int IN_DT, int FMT>
 int tw_launch(const void *x, int64_t n, const float *scale, uint8_t *q, float *scale_inv,
               float *parts, bool vec, hipStream_t st) {
+    if (scale == nullptr && vec && n > 0 && n <= TW_FUSED_MAX) {
+        // a captured call would replay its tag: under stream capture the
+        // two-launch form below is used
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        PTA_CHECK_HIP(hipStreamIsCapturing(st, &cs));
+        if (cs == hipStreamCaptureStatusNone) return tw_fused_launch<IN_DT, FMT>(x, n, q, scale_inv, parts, st);
+    }
     const int g = tw_grid(n);
     if (scale == nullptr) {
         if (vec) tw_amax_kernel<IN_DT, true><<<g, NT, 0, st>>>(x, n, parts);

@@ -75,6 +75,22 @@ def test_tensorwise_every_bf16_value(qdt):
     assert_bytes_equal(u8(q), exp, "rne bytes")
 
 
+@pytest.mark.parametrize("n", [(1 << 19) + 5, (1 << 20) + 5, (1 << 21) - 7, 1 << 21, (1 << 21) + 16])
+@pytest.mark.parametrize("spike", [0, -1, "mid"])
+def test_tensorwise_single_launch_sizes(n, spike):
+    """Sizes around the single-launch form's limits (16, 32 and 64 elements per
+    thread, and the first size that takes the two-launch form): one spike
+    anywhere, including the last workgroup's last element, sets the scale."""
+    turbo, SG, _ = _turbo()
+    x = _input((n,), seed=11)
+    pos = n // 2 + 3 if spike == "mid" else spike
+    x[pos] = -1000.0
+    q, s = turbo.ops.quantize_fp8(x.cuda(), torch.float8_e4m3fn, SG.TENSORWISE)
+    qo, so = O.quant_tensorwise(x, FMT[torch.float8_e4m3fn])
+    assert_f32_bitexact(f32(s), so, "scale_inv")
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+
+
 @pytest.mark.parametrize("n", [1, 4096, 1 << 20, (1 << 20) + 13])
 @pytest.mark.parametrize("qdt", FP8)
 def test_tensorwise_vs_reference_kernels(n, qdt):
