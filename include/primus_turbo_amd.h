@@ -67,7 +67,7 @@ size_t pta_quantize_fp8_tensorwise_workspace_size(int64_t n);
  * is a device scalar used instead of the amax-derived one.  Up to 2^21
  * elements (16-byte aligned x and q, stream not capturing) this is one launch
  * whose workgroups exchange partial maxima through the workspace; if that
- * exchange does not complete, *scale_inv is NaN.  Otherwise two launches. */
+ * exchange does not complete, *scale_inv is NaN.  Otherwise two launches.
  * Replaces quantize_fp8_tensorwise (csrc/pytorch/quantization/quantization.cpp:42-88). */
 int pta_quantize_fp8_tensorwise(const void *x, int in_dtype, int64_t n, const float *scale,
                                 void *q, int fmt, float *scale_inv, void *workspace,
