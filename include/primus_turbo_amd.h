@@ -273,7 +273,10 @@ int pta_grouped_compute_padded_offs(const int64_t *offs, int64_t *padded_offs, i
  *   NN: A[M,K] a_scale[M,K/128];  B[K,N] b_scale[K/128,N/128]
  *   TN: A[K,M] a_scale[K/128,M];  B[K,N] b_scale[K/128,N]
  * workspace may be NULL when pta_gemm_fp8_workspace_size() returns 0 for
- * these arguments.  Replaces gemm_fp8_impl
+ * these arguments.  The workspace holds the NN / TN operand transposes and,
+ * for problems of at most half a round of 256 x 256 tiles with K >= 1024 and
+ * K % 128 == 0, the fp32 partial tiles of the K split (each tile then runs as
+ * two half-K workgroups; not under stream capture).  Replaces gemm_fp8_impl
  * (primus_turbo/pytorch/kernels/gemm/gemm_fp8_impl.py:438-467) and the native
  * hipblaslt/ck/turbo_gemm_fp8 ops behind it. */
 size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b,

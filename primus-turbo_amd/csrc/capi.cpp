@@ -1,4 +1,8 @@
 // Error state and version of the C ABI (include/primus_turbo_amd.h).
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 
@@ -16,6 +20,36 @@ void set_error(const char *fmt, ...) {
 }
 
 void clear_error() { g_last_error[0] = '\0'; }
+
+uint64_t next_call_tag() {
+    static std::atomic<uint64_t> ctr{0};
+    static const uint64_t        salt =
+        (static_cast<uint64_t>(getpid()) << 40) ^
+        (static_cast<uint64_t>(std::chrono::steady_clock::now().time_since_epoch().count()) << 16);
+    return salt ^ (ctr.fetch_add(1, std::memory_order_relaxed) + 1);
+}
+
+bool stream_capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    // an error (e.g. a legacy-stream query during another stream's capture)
+    // counts as capturing: the caller then takes its graph-safe form
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return true;
+    return cs != hipStreamCaptureStatusNone;
+}
+
+int device_cu_count() {
+    constexpr int   kMax = 64;
+    static std::atomic<int> cus[kMax] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+    if (dev < kMax) {
+        if (int c = cus[dev].load(std::memory_order_relaxed)) return c;
+    }
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    if (dev < kMax) cus[dev].store(c, std::memory_order_relaxed);
+    return c;
+}
 
 } // namespace pta
 

@@ -49,6 +49,19 @@ inline float fp8_max_host(int fmt) { return fmt == PTA_E5M2 ? 57344.0f : 448.0f;
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// 64-bit tag unique per call within the process (a per-process salt from the
+// process id and start time, xor a counter): kernels whose workgroups hand data
+// to each other through a caller's workspace mark each handover with it, so a
+// workspace holding an earlier call's tags needs no clearing.
+uint64_t next_call_tag();
+
+// true when work submitted to st is being recorded into a graph (a recorded
+// call tag would repeat on every replay)
+bool stream_capturing(hipStream_t st);
+
+// compute units of the current device (cached per device)
+int device_cu_count();
+
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------

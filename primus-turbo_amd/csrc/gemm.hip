@@ -29,11 +29,31 @@
 namespace pta {
 using namespace gemm_detail;
 
+// K split for problems of at most half a round of tiles (one 256 x 256 tile
+// per CU and round): every tile runs as two half-K workgroups whose fp32
+// partials meet in the workspace, so twice as many CUs work.  The hand-over
+// (256 KB written and read per tile) costs about 15% of a half-length tile;
+// splitting the last round of larger problems measured no faster (headline
+// 4096x18432x7168: +1%), so those run whole.  Returns the number of split
+// tiles (0: none).
+int64_t split_tiles(int64_t tiles, int64_t K, int cus) {
+    if (K % BK != 0 || K / BK < 8 || tiles <= 0 || cus <= 0) return 0;
+    return 2 * tiles <= cus ? tiles : 0;
+}
+
+constexpr int64_t SPLIT_TILE_BYTES = int64_t(BM) * BN * 4;
+
+// workspace bytes for `n` split tiles (fp32 partial tiles, then one tag each)
+int64_t split_ws_bytes(int64_t n) { return n > 0 ? n * SPLIT_TILE_BYTES + cdiv(n * 8, 256) * 256 : 0; }
+
 // Entry used by the dense and grouped front ends: NT problem fully described.
+// split_ws: workspace of split_ws_bytes(split_tiles(...)) bytes, or NULL (no
+// K split).
 int gemm_nt_launch(const uint8_t *a, int fa, int64_t lda, const uint8_t *b, int fb, int64_t ldb,
                    void *c, int out_dt, int64_t ldc, int64_t M, int64_t N, int64_t K, int sm,
                    bool a2d, bool b2d, const void *sa, int64_t sa_m, int64_t sa_k, int64_t sa_bytes,
-                   const void *sb, int64_t sb_m, int64_t sb_k, int64_t sb_bytes, hipStream_t st) {
+                   const void *sb, int64_t sb_m, int64_t sb_k, int64_t sb_bytes, hipStream_t st,
+                   uint8_t *split_ws = nullptr) {
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c; g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
     g.sa = sa; g.sb = sb; g.sa_m = sa_m; g.sa_k = sa_k; g.sb_m = sb_m; g.sb_k = sb_k;
@@ -46,6 +66,16 @@ int gemm_nt_launch(const uint8_t *a, int fa, int64_t lda, const uint8_t *b, int 
     g.tiles_n = static_cast<int>(cdiv(N, BN));
     g.group_m = 4;
     g.aligned_c = ((ldc * (out_dt == PTA_F32 ? 4 : 2)) % 16 == 0) && aligned16(c);
+    if (split_ws != nullptr && !stream_capturing(st)) {
+        // a graph would replay the call tag, so captured calls do not split
+        const int64_t ns = split_tiles(int64_t(g.tiles_m) * g.tiles_n, K, device_cu_count());
+        if (ns > 0) {
+            g.split_count = static_cast<int>(ns);
+            g.split_ws    = reinterpret_cast<float *>(split_ws);
+            g.split_tags  = reinterpret_cast<uint64_t *>(split_ws + ns * SPLIT_TILE_BYTES);
+            g.split_tag   = next_call_tag();
+        }
+    }
     if (sm == SM_TENSOR) return dispatch_tensor(g, fa, fb, out_dt, st);
     if (sm == SM_ROW) return dispatch_row(g, fa, fb, out_dt, st);
     if (sm == SM_MX) return dispatch_mx(g, fa, fb, out_dt, st);
@@ -164,6 +194,7 @@ extern "C" size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, i
     size_t ws = 0;
     if (trans_a) ws += static_cast<size_t>(cdiv(M * K, 256) * 256);
     if (!trans_b) ws += static_cast<size_t>(cdiv(N * K, 256) * 256);
+    ws += static_cast<size_t>(split_ws_bytes(split_tiles(cdiv(M, BM) * cdiv(N, BN), K, device_cu_count())));
     return ws;
 }
 
@@ -213,7 +244,10 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
     if (!trans_b) { // B stored [K, N]
         if (int rc = pta_transpose_u8(b, 1, K, N, wsp, stream)) return rc;
         bp = wsp;
+        wsp += cdiv(N * K, 256) * 256;
     }
+    // what remains of the workspace holds the K split's partial tiles
+    uint8_t *split_ws = split_tiles(cdiv(M, BM) * cdiv(N, BN), K, device_cu_count()) > 0 ? wsp : nullptr;
     // scale strides in the NT view
     bool    a2d = false, b2d = false;
     int64_t sa_m = 0, sa_k = 0, sb_m = 0, sb_k = 0;
@@ -237,11 +271,11 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
     if (sm == SM_MX) { sa_bytes = M * (K / 32); sb_bytes = N * (K / 32); }
     if (!trans_c) {
         return gemm_nt_launch(ap, a_fmt, K, bp, b_fmt, K, c, c_dtype, N, M, N, K, sm, a2d, b2d,
-                              a_scale, sa_m, sa_k, sa_bytes, b_scale, sb_m, sb_k, sb_bytes, st);
+                              a_scale, sa_m, sa_k, sa_bytes, b_scale, sb_m, sb_k, sb_bytes, st, split_ws);
     }
     // C^T[n, m] = sum_k B'[n,k] A'[m,k]: swap the operands
     return gemm_nt_launch(bp, b_fmt, K, ap, a_fmt, K, c, c_dtype, M, N, M, K, sm, b2d, a2d,
-                          b_scale, sb_m, sb_k, sb_bytes, a_scale, sa_m, sa_k, sa_bytes, st);
+                          b_scale, sb_m, sb_k, sb_bytes, a_scale, sa_m, sa_k, sa_bytes, st, split_ws);
 }
 
 extern "C" int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt,

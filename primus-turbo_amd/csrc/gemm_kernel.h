@@ -87,7 +87,19 @@ struct GemmArgs {
     int64_t        G;
     int64_t        b_gstride, sb_gstride, c_gstride; // elements / bytes per group
     int            persistent; // > 0: a grid of that many workgroups loops over the tiles_m * tiles_n tiles
+    // K split of the last split_count tiles of the tile order (dense,
+    // non-persistent; 0: none).  With W = tiles_m * tiles_n - split_count whole
+    // tiles, split tile q runs as workgroups W + 2 q (K blocks [0, nk/2)) and
+    // W + 2 q + 1 (the rest).  The first writes its fp32 accumulators to
+    // split_ws[q] and then split_tags[q] = split_tag; the second waits for
+    // that tag, adds them and stores C.
+    int       split_count;
+    float    *split_ws;   // 256 x 256 fp32 per split tile
+    uint64_t *split_tags; // one per split tile
+    uint64_t  split_tag;  // unique per call
 };
+
+constexpr unsigned SPLIT_SPIN_LIMIT = 1u << 22; // polls (s_sleep 2 apart) before the wait gives up
 
 // gfx950 serves a ds_read_b128 two 8-lane groups per clock; with the chunk
 // XORed by row % 8 the 16-row fragment reads hit every bank once per clock.
@@ -267,7 +279,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
     const uint8_t *A = g.a, *B = g.b;
     const void    *SB = g.sb;
     void          *C  = g.c;
-    int64_t        kb_base = 0; // first global K block of this problem (group_mode 2)
+    int64_t        kb_base = 0; // first global K block of this problem (group_mode 2, K split)
+    int            split_half = -1, split_q = 0; // K-split tile: which half, which split tile
     if (g.group_mode == 1) {
         // XCD-aware order: workgroups are dispatched round-robin over the 8
         // XCDs.  M-tile rows go in blocks of 32: XCD x takes rows 4x .. 4x+3
@@ -300,7 +313,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
     } else {
         int       id    = static_cast<int>(bid);
         const int total = g.tiles_m * g.tiles_n;
-        if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+        const int whole = PERSIST ? total : total - g.split_count;
+        if (id >= whole) {
+            // K-split tiles follow the whole ones in tile order.  Workgroups go
+            // round-robin over the 8 XCDs: XCD x takes a contiguous range of
+            // the split tiles, both halves of each (half 0 at workgroup p, half
+            // 1 at p + 8, so the half that waits was dispatched second)
+            int q = id - whole;
+            if ((g.split_count & 7) == 0) {
+                const int x = q & 7, slot = q >> 3;
+                split_half  = slot & 1;
+                split_q     = x * (g.split_count >> 3) + (slot >> 1);
+            } else {
+                split_half = q & 1;
+                split_q    = q >> 1;
+            }
+            id = whole + split_q;
+        } else if ((whole & 7) == 0) {
+            id = (id & 7) * (whole >> 3) + (id >> 3);
+        }
         const int per_group = g.group_m * g.tiles_n;
         const int grp       = id / per_group;
         const int first_m   = grp * g.group_m;
@@ -318,6 +349,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
             B       = g.b + k0;
             kb_base = k0 / BK;
             C       = reinterpret_cast<uint8_t *>(g.c) + q * g.c_gstride;
+        }
+        if (split_half >= 0) {
+            // K % BK == 0 here; the second half starts at K block nk / 2
+            const int64_t kh = (K / BK) / 2;
+            if (split_half == 0) {
+                K = kh * BK;
+            } else {
+                A += kh * BK;
+                B += kh * BK;
+                K -= kh * BK;
+                kb_base += kh;
+            }
         }
     }
     const int nk = static_cast<int>((K + BK - 1) / BK);
@@ -554,6 +597,64 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
         }
     }
 
+    // ---- K split: the first half hands its accumulators to the second -------
+    if constexpr (!PERSIST) {
+        if (split_half >= 0) {
+            // 16 bytes per lane and sub-tile, lane-contiguous (1 KB per wave and
+            // instruction; the sub-tile's offset goes in the scalar offset);
+            // device-coherent (sc1) stores and loads, since the two halves may
+            // run on different XCDs
+            constexpr int SPLIT_BYTES = BM * BN_ * 4;
+            const rsrc_t  rW = make_rsrc(reinterpret_cast<uint8_t *>(g.split_ws) + int64_t(split_q) * SPLIT_BYTES,
+                                         SPLIT_BYTES);
+            constexpr int SC1 = 16; // cache-policy bit: coherent at device scope
+            if (split_half == 0) {
+#pragma unroll
+                for (int j = 0; j < TN_; ++j)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc[j][i]), rW, t * 16,
+                                                               (j * TM + i) * NTHR * 16, SC1);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads(); // every lane's stores have completed
+                if (t == 0)
+                    __hip_atomic_store(&g.split_tags[split_q], g.split_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
+            // second half: its partner has a lower workgroup id, so it was
+            // dispatched first; the wait is bounded and a timeout gives NaN
+            bool seen = true;
+            if (t == 0) {
+                unsigned k = 0;
+                while (__hip_atomic_load(&g.split_tags[split_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+                           g.split_tag &&
+                       k < SPLIT_SPIN_LIMIT) {
+                    ++k;
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                seen = k < SPLIT_SPIN_LIMIT;
+            }
+            const float bad = __syncthreads_or(!seen) ? __builtin_nanf("") : 0.0f;
+            // two batches of loads, so their registers fit beside the accumulators
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                v4f part[TN_ / 2][TM];
+#pragma unroll
+                for (int jj = 0; jj < TN_ / 2; ++jj)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        part[jj][i] = __builtin_bit_cast(
+                            v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                     rW, t * 16, ((h * TN_ / 2 + jj) * TM + i) * NTHR * 16, SC1));
+#pragma unroll
+                for (int jj = 0; jj < TN_ / 2; ++jj)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) acc[h * TN_ / 2 + jj][i] += part[jj][i] + bad;
+                asm volatile("" ::: "memory");
+            }
+        }
+    }
+
     // ---- epilogue -----------------------------------------------------------
     if constexpr (OUT_DT != PTA_F32) {
         // full tiles: convert in registers, stage the 256 x 256 tile in LDS,
@@ -684,7 +785,7 @@ int launch_kernel(const GemmArgs &g, hipStream_t st) {
     }
     const uint32_t ntiles = static_cast<uint32_t>(g.tiles_m * g.tiles_n);
     const uint32_t np     = static_cast<uint32_t>(g.persistent);
-    const dim3     grid(g.persistent > 0 ? (np < ntiles ? np : ntiles) : ntiles,
+    const dim3     grid(g.persistent > 0 ? (np < ntiles ? np : ntiles) : ntiles + static_cast<uint32_t>(g.split_count),
                         static_cast<uint32_t>(g.group_mode == 2 ? g.G : 1));
     kern<<<grid, NTHR, smem, st>>>(g);
     PTA_CHECK_LAUNCH();

@@ -14,10 +14,6 @@
 //   e8m0 = clamp(E + 127, 0, 254), q = fp8(x * 2^(127 - e8m0)).
 #include "common.h"
 
-#include <unistd.h>
-
-#include <atomic>
-#include <chrono>
 #include <mutex>
 
 namespace pta {
@@ -199,22 +195,13 @@ __global__ __launch_bounds__(NT) void tw_fused_kernel(const void *x, int64_t n, 
     }
 }
 
-// per-call tags: a per-process salt (process id, start time) xor a counter
-uint64_t tw_next_tag() {
-    static std::atomic<uint64_t> ctr{0};
-    static const uint64_t        salt =
-        (static_cast<uint64_t>(getpid()) << 40) ^
-        (static_cast<uint64_t>(std::chrono::steady_clock::now().time_since_epoch().count()) << 16);
-    return salt ^ (ctr.fetch_add(1, std::memory_order_relaxed) + 1);
-}
-
 template <int IN_DT, int FMT>
 int tw_fused_launch(const void *x, int64_t n, uint8_t *q, float *scale_inv, float *parts, hipStream_t st) {
     const int64_t per  = static_cast<int64_t>(NT) * 16;
     const int     it   = n <= per * TW_FUSED_GRID ? 1 : n <= 2 * per * TW_FUSED_GRID ? 2 : 4;
     const int     g    = static_cast<int>(std::max<int64_t>(1, cdiv(n, per * it)));
     uint64_t     *tags = reinterpret_cast<uint64_t *>(reinterpret_cast<uint8_t *>(parts) + TW_TAG_OFFSET);
-    const uint64_t tag = tw_next_tag();
+    const uint64_t tag = next_call_tag();
     if (it == 1) tw_fused_kernel<IN_DT, FMT, 1><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
     else if (it == 2) tw_fused_kernel<IN_DT, FMT, 2><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
     else tw_fused_kernel<IN_DT, FMT, 4><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
@@ -705,9 +692,7 @@ int tw_launch(const void *x, int64_t n, const float *scale, uint8_t *q, float *s
     if (scale == nullptr && vec && n > 0 && n <= TW_FUSED_MAX) {
         // a captured call would replay its tag: under stream capture the
         // two-launch form below is used
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        PTA_CHECK_HIP(hipStreamIsCapturing(st, &cs));
-        if (cs == hipStreamCaptureStatusNone) return tw_fused_launch<IN_DT, FMT>(x, n, q, scale_inv, parts, st);
+        if (!stream_capturing(st)) return tw_fused_launch<IN_DT, FMT>(x, n, q, scale_inv, parts, st);
     }
     const int g = tw_grid(n);
     if (scale == nullptr) {

@@ -110,6 +110,54 @@ def test_gemm_blockwise_vs_oracle(mnk, layout, qdt):
     _check(out, ref, f"BLOCKWISE {layout}")
 
 
+@pytest.mark.parametrize("mnk", [(2304, 3072, 2048), (2300, 3000, 1024), (4096, 2048, 7168), (2048, 4352, 1152)])
+@pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
+def test_gemm_k_split_vs_oracle(mnk, gran):
+    """Problems of 72-128 tiles of 256 x 256 with K >= 1024 run every tile as two
+    half-K workgroups (fp32 partials handed over through the workspace),
+    including partial edge tiles: the result meets the oracle criterion and
+    matches the unsplit strided entry (same operands) to within fp32 summation
+    order, and a repeated call gives the same bits."""
+    turbo, _, _, _, SG, SR, gemm_fp8_impl = _mods()
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_nt
+    from primus_turbo.pytorch.ops.gemm_fp8 import _mx_strides
+
+    g = getattr(SG, gran)
+    M, N, K = mnk
+    qdt = torch.float8_e4m3fn
+    a = randn((M, K), seed=21, outliers=0.001).cuda()
+    b = randn((N, K), seed=22, outliers=0.001).cuda()
+    kb = (K + 127) // 128
+    if g == SG.TENSORWISE:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g)
+        da, db = O.dequant_tensorwise(u8(qa), 0, f32(sa)), O.dequant_tensorwise(u8(qb), 0, f32(sb))
+        nt = dict(a_scale=sa, b_scale=sb)
+    elif g == SG.ROWWISE:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g, axis=-1)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g, axis=-1)
+        da, db = O.dequant_rowwise(u8(qa), 0, f32(sa)), O.dequant_rowwise(u8(qb), 0, f32(sb))
+        nt = dict(a_scale=sa, b_scale=sb)
+    elif g == SG.BLOCKWISE:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g, block_size=128, axis=1)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g, block_size=128, scaling_recipe=SR(use_2d_block=True))
+        da, db = O.dequant_block1d(u8(qa), 0, f32(sa), 1), O.dequant_block2d(u8(qb), 0, f32(sb))
+        nt = dict(a_scale=sa, sa_strides=(kb, 1), b_scale=sb, sb_strides=(kb, 1), b_scale_2d=True)
+    else:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g, block_size=32, axis=1, scaling_recipe=SR())
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g, block_size=32, axis=1, scaling_recipe=SR(use_2d_block=True))
+        da, db = O.dequant_mx(u8(qa), 0, u8(sa)), O.dequant_mx(u8(qb), 0, u8(sb))
+        nt = dict(a_scale=sa, sa_strides=_mx_strides(sa), b_scale=sb, sb_strides=_mx_strides(sb))
+    out = gemm_fp8_impl(qa, sa, False, qb, sb, True, torch.bfloat16, False, g.value)
+    again = gemm_fp8_impl(qa, sa, False, qb, sb, True, torch.bfloat16, False, g.value)
+    whole = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt)[:, :N]
+    ref = O.gemm_ref(da, db, False, True)
+    _check(out, ref, f"{gran} split")
+    assert torch.equal(out, again), "split GEMM is not deterministic"
+    o, w = f32(out).astype(np.float64), f32(whole).astype(np.float64)
+    assert np.max(np.abs(o - w)) <= 2.0 ** -6 * np.max(np.abs(w)), "split and whole results differ beyond rounding"
+
+
 @pytest.mark.parametrize("mnk", [(256, 512, 512), (176, 352, 160), (1024, 1024, 1024)])
 @pytest.mark.parametrize("fmts", [(torch.float8_e4m3fn, torch.float8_e4m3fn), (torch.float8_e5m2, torch.float8_e4m3fn)])
 def test_gemm_mx_vs_oracle(mnk, fmts):
