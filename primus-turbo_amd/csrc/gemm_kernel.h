@@ -269,7 +269,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
     int t = threadIdx.x;
     if constexpr (PERSIST) asm volatile("" : "+v"(t));
     const int lane = t & 63;
-    const int wave = t >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6); // wave-uniform: scalar tile addressing
     const int wm   = wave / WGN;
     const int wn   = wave % WGN;
 
@@ -635,21 +635,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
                 seen = k < SPLIT_SPIN_LIMIT;
             }
             const float bad = __syncthreads_or(!seen) ? __builtin_nanf("") : 0.0f;
-            // two batches of loads, so their registers fit beside the accumulators
+            // batches of loads small enough for their registers to fit beside
+            // the accumulators
+            constexpr int NB = 4, JB = TN_ / NB;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                v4f part[TN_ / 2][TM];
+            for (int h = 0; h < NB; ++h) {
+                v4f part[JB][TM];
 #pragma unroll
-                for (int jj = 0; jj < TN_ / 2; ++jj)
+                for (int jj = 0; jj < JB; ++jj)
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
                         part[jj][i] = __builtin_bit_cast(
-                            v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                                     rW, t * 16, ((h * TN_ / 2 + jj) * TM + i) * NTHR * 16, SC1));
+                            v4f, __builtin_amdgcn_raw_buffer_load_b128(rW, t * 16, ((h * JB + jj) * TM + i) * NTHR * 16,
+                                                                       SC1));
 #pragma unroll
-                for (int jj = 0; jj < TN_ / 2; ++jj)
+                for (int jj = 0; jj < JB; ++jj)
 #pragma unroll
-                    for (int i = 0; i < TM; ++i) acc[h * TN_ / 2 + jj][i] += part[jj][i] + bad;
+                    for (int i = 0; i < TM; ++i) acc[h * JB + jj][i] += part[jj][i] + bad;
                 asm volatile("" ::: "memory");
             }
         }
