@@ -496,9 +496,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
 
     // blockwise pipeline state: partial buffers p[4]; the two tiles issued last
     // in a K block are scaled at the start of the next one with that block's scales
-    v4f   p[4];
-    float s_pend[4];
-    bool  have_pend = false;
+    v4f    p[4];
+    float  s_pend[4];
+    v4f    pend4[2];
+    float4 sbj_prev = make_float4(0.f, 0.f, 0.f, 0.f);
+    bool   have_pend = false;
 
     for (int kb = 0; kb < nk; ++kb) {
         const int cur = kb & 1;
@@ -547,11 +549,29 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
                             acc[q / TM][q % TM] += p[q & 3] * s_pend[q & 3];
                         }
                     } else {
-                        const float sa_i = sc_cur.sa[i];
-                        acc[j][i][0] += p[tt & 3][0] * (sa_i * sbj.x);
-                        acc[j][i][1] += p[tt & 3][1] * (sa_i * sbj.y);
-                        acc[j][i][2] += p[tt & 3][2] * (sa_i * sbj.z);
-                        acc[j][i][3] += p[tt & 3][3] * (sa_i * sbj.w);
+                        // 1-D B scales: the tile issued two MFMAs earlier, whose B
+                        // scales are this fragment's (i >= 2) or the previous
+                        // one's (i < 2); deferring it was 7% faster than scaling
+                        // each partial right behind its MFMA
+                        if (tt >= 2) {
+                            const int    q  = tt - 2, iq = q % TM;
+                            const float4 sq = q / TM == j ? sbj : sbj_prev;
+                            const float  sa = sc_cur.sa[iq];
+                            acc[q / TM][iq][0] += p[q & 3][0] * (sa * sq.x);
+                            acc[q / TM][iq][1] += p[q & 3][1] * (sa * sq.y);
+                            acc[q / TM][iq][2] += p[q & 3][2] * (sa * sq.z);
+                            acc[q / TM][iq][3] += p[q & 3][3] * (sa * sq.w);
+                        } else if (have_pend) {
+                            const int q = TN_ * TM - 2 + tt;
+                            acc[q / TM][q % TM] += p[q & 3] * pend4[tt];
+                        }
+                        // per MFMA: the MFMA, four VALU, (first MFMA of each B
+                        // fragment) the next fragment's LDS reads and its B
+                        // scales, four VALU (4% faster than the compiler's order)
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0); // VALU
+                        if (i == 0) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0); // DS read
+                        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0); // VALU
                     }
                     if constexpr (B2D) {
                         // instruction order per MFMA: the MFMA, two VALU, (first
@@ -572,16 +592,26 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
                         bf, af[i], acc[j][i], FB, FA, 0, 0, 0, 0);
                     // the next B fragment's LDS reads go behind the second MFMA
                     // of each fragment (4% faster than the compiler's order; the
-                    // same pattern measured slower for MX and for 1-D B scales)
+                    // same pattern measured slower for MX)
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
                     if (i == 1) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); // DS read
                 }
             }
             bf = bn;
+            sbj_prev = sbj;
         }
         if constexpr (SM == SM_BLOCK && B2D) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) s_pend[q] = s_i[q % TM];
+            have_pend = true;
+        }
+        if constexpr (SM == SM_BLOCK && !B2D) {
+            // tiles 30, 31 (fragment 7, i = 2, 3) are scaled in the next step
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float sa = sc_cur.sa[TM - 2 + u];
+                pend4[u] = v4f{sa * sbj_prev.x, sa * sbj_prev.y, sa * sbj_prev.z, sa * sbj_prev.w};
+            }
             have_pend = true;
         }
         sc_cur = sc_nxt;
@@ -593,6 +623,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
             for (int tt = 0; tt < 2; ++tt) {
                 const int q = TN_ * TM - 2 + tt;
                 acc[q / TM][q % TM] += p[q & 3] * s_pend[q & 3];
+            }
+        }
+    }
+    if constexpr (SM == SM_BLOCK && !B2D) {
+        if (have_pend) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int q = TN_ * TM - 2 + tt;
+                acc[q / TM][q % TM] += p[q & 3] * pend4[tt];
             }
         }
     }
