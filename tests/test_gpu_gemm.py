@@ -110,12 +110,13 @@ def test_gemm_blockwise_vs_oracle(mnk, layout, qdt):
     _check(out, ref, f"BLOCKWISE {layout}")
 
 
-@pytest.mark.parametrize("mnk", [(2304, 3072, 2048), (2300, 3000, 1024), (4096, 2048, 7168), (2048, 4352, 1152)])
+@pytest.mark.parametrize("mnk", [(2304, 3072, 2048), (2300, 3000, 1024), (4096, 2048, 7168), (2048, 4352, 1152), (1024, 4096, 4096)])
 @pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
 def test_gemm_k_split_vs_oracle(mnk, gran):
-    """Problems of 72-128 tiles of 256 x 256 with K >= 1024 run every tile as two
-    half-K workgroups (fp32 partials handed over through the workspace),
-    including partial edge tiles: the result meets the oracle criterion and
+    """Problems of 72-128 tiles of 256 x 256 with K >= 1024 (from 48 tiles with
+    K >= 4096 and K-contiguous operands) run every tile as two half-K
+    workgroups (fp32 partials handed over through the workspace), including
+    partial edge tiles: the result meets the oracle criterion and
     matches the unsplit strided entry (same operands) to within fp32 summation
     order, and a repeated call gives the same bits."""
     turbo, _, _, _, SG, SR, gemm_fp8_impl = _mods()
