@@ -159,6 +159,33 @@ def test_gemm_k_split_vs_oracle(mnk, gran):
     assert np.max(np.abs(o - w)) <= 2.0 ** -6 * np.max(np.abs(w)), "split and whole results differ beyond rounding"
 
 
+@pytest.mark.parametrize("gran", ["TENSORWISE", "BLOCKWISE"])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("trans_c", [False, True])
+def test_gemm_k_split_out_dtype_trans_c(gran, out_dtype, trans_c):
+    """The K-split finisher writes through the same epilogue as a whole tile:
+    fp32 and fp16 outputs and the transposed output (operands exchanged) meet
+    the oracle criterion on a 108-tile problem with a partial edge tile."""
+    turbo, _, _, _, SG, SR, gemm_fp8_impl = _mods()
+    g = getattr(SG, gran)
+    M, N, K = 2300, 3000, 2048
+    qdt = torch.float8_e4m3fn
+    a = randn((M, K), seed=31, outliers=0.001).cuda()
+    b = randn((N, K), seed=32, outliers=0.001).cuda()
+    if g == SG.TENSORWISE:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g)
+        da, db = O.dequant_tensorwise(u8(qa), 0, f32(sa)), O.dequant_tensorwise(u8(qb), 0, f32(sb))
+    else:
+        qa, sa = turbo.ops.quantize_fp8(a, qdt, g, block_size=128, axis=1)
+        qb, sb = turbo.ops.quantize_fp8(b, qdt, g, block_size=128, scaling_recipe=SR(use_2d_block=True))
+        da, db = O.dequant_block1d(u8(qa), 0, f32(sa), 1), O.dequant_block2d(u8(qb), 0, f32(sb))
+    out = gemm_fp8_impl(qa, sa, False, qb, sb, True, out_dtype, trans_c, g.value)
+    ref = O.gemm_ref(da, db, False, True, trans_c)
+    assert out.dtype == out_dtype and tuple(out.shape) == ref.shape
+    _check(out, ref, f"{gran} split {out_dtype} trans_c={trans_c}")
+
+
 @pytest.mark.parametrize("mnk", [(256, 512, 512), (176, 352, 160), (1024, 1024, 1024)])
 @pytest.mark.parametrize("fmts", [(torch.float8_e4m3fn, torch.float8_e4m3fn), (torch.float8_e5m2, torch.float8_e4m3fn)])
 def test_gemm_mx_vs_oracle(mnk, fmts):
