@@ -274,7 +274,7 @@ int pta_grouped_compute_padded_offs(const int64_t *offs, int64_t *padded_offs, i
  *   TN: A[K,M] a_scale[K/128,M];  B[K,N] b_scale[K/128,N]
  * workspace may be NULL when pta_gemm_fp8_workspace_size() returns 0 for
  * these arguments.  The workspace holds the NN / TN operand transposes and,
- * for problems of at most half a round of 256 x 256 tiles with K >= 1024 and
+ * for problems of at most half a round of 256 x 256 tiles with K >= 4096 and
  * K % 128 == 0, the fp32 partial tiles of the K split (each tile then runs as
  * two half-K workgroups; not under stream capture).  Replaces gemm_fp8_impl
  * (primus_turbo/pytorch/kernels/gemm/gemm_fp8_impl.py:438-467) and the native
@@ -303,6 +303,29 @@ int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b
                             int64_t sa_k, int a_scale_2d, int64_t a_scale_bytes,
                             const void *b_scale, int64_t sb_m, int64_t sb_k, int b_scale_2d,
                             int64_t b_scale_bytes, pta_stream_t stream);
+
+/* pta_gemm_fp8_nt_strided with the kernel choice of pta_gemm_fp8: problems of
+ * fewer than 72 tiles of 256 x 256 run on the small-tile kernel (results bit
+ * for bit those of the 256 x 256 kernel; blockwise problems it would run on
+ * 128 x 128 tiles stay on the 256 x 256 kernel), and problems of at most half
+ * a round of tiles with K >= 4096 and K % 128 == 0 take the K split, whose
+ * fp32 partial tiles and per-call tags live in the workspace (not under
+ * stream capture; two calls in flight must not share one workspace).  The
+ * workspace size depends on the shape, the granularity, the row strides and
+ * the scale extents: pta_gemm_fp8_nt_strided_ws_size(); workspace may be NULL
+ * when that is 0.
+ * The strided entry above always runs the 256 x 256 kernel.  Like it, this has
+ * no single counterpart in the reference: it is what the autograd functions
+ * below gemm_fp8_impl call. */
+size_t pta_gemm_fp8_nt_strided_ws_size(int64_t M, int64_t N, int64_t K, int granularity, int64_t lda,
+                                       int64_t ldb, int64_t a_scale_bytes, int64_t b_scale_bytes);
+int pta_gemm_fp8_nt_strided_ws(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt,
+                               int64_t ldb, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N,
+                               int64_t K, int granularity, const void *a_scale, int64_t sa_m,
+                               int64_t sa_k, int a_scale_2d, int64_t a_scale_bytes,
+                               const void *b_scale, int64_t sb_m, int64_t sb_k, int b_scale_2d,
+                               int64_t b_scale_bytes, void *workspace, size_t workspace_bytes,
+                               pta_stream_t stream);
 
 /* Grouped GEMM over G groups of rows of A (M-grouped, forward / dgrad):
  * out[offs[g]:offs[g+1]] = A[offs[g]:offs[g+1]] @ op(B[g]), B[G, N, K]

@@ -30,14 +30,16 @@ namespace pta {
 using namespace gemm_detail;
 
 // K split for problems of at most half a round of tiles (one 256 x 256 tile
-// per CU and round): every tile runs as two half-K workgroups whose fp32
-// partials meet in the workspace, so twice as many CUs work.  The hand-over
-// (256 KB written and read per tile) costs about 15% of a half-length tile;
-// splitting the last round of larger problems measured no faster (headline
+// per CU and round) and K >= 4096: every tile runs as two half-K workgroups
+// whose fp32 partials meet in the workspace, so twice as many CUs work.  The
+// hand-over (256 KB written and read per tile) costs a fixed ~6-10 us, so a
+// shorter K runs whole (108 tiles, split / whole: K = 2048 1.22-1.27, 3072
+// 1.01-1.04, 4096 0.92-0.98, 6144 0.78-0.80; 64 tiles at K = 4096: 0.78-0.81).
+// Splitting the last round of larger problems measured no faster (headline
 // 4096x18432x7168: +1%), so those run whole.  Returns the number of split
 // tiles (0: none).
 int64_t split_tiles(int64_t tiles, int64_t K, int cus) {
-    if (K % BK != 0 || K / BK < 8 || tiles <= 0 || cus <= 0) return 0;
+    if (K % BK != 0 || K < 4096 || tiles <= 0 || cus <= 0) return 0;
     return 2 * tiles <= cus ? tiles : 0;
 }
 
@@ -108,6 +110,9 @@ __global__ void zero_fill_kernel(uint8_t *c, int64_t bytes) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes; i += stride) c[i] = 0;
 }
 
+int small_dispatch(gemm_small::SmallArgs &g, bool akm, bool bkm, int fa, int fb, int c_dtype, int sm,
+                   hipStream_t st);
+
 // pta_gemm_fp8 on the small-tile kernel: operands read in place (K-major for
 // trans_a A and for non-trans_b B), scale strides as the reference's layouts
 // give them, C^T by exchanging the operands.
@@ -147,6 +152,13 @@ int gemm_small_nt(const void *a, int a_fmt, const void *a_scale, int trans_a, co
         std::swap(akm, bkm); std::swap(fa, fb);
         g.ldc = M;
     }
+    return small_dispatch(g, akm, bkm, fa, fb, c_dtype, sm, st);
+}
+
+// Tile choice, tile order and launch of the small-tile kernel for a problem
+// in the NT view (g without tile, tiles_*, group_m and aligned_c).
+int small_dispatch(gemm_small::SmallArgs &g, bool akm, bool bkm, int fa, int fb, int c_dtype, int sm,
+                   hipStream_t st) {
     // the largest tile whose grid still covers the CUs (a K-major operand's
     // row stride must be a multiple of the tile's bytes per K row and thread)
     using gemm_small::TILE_32x64;
@@ -166,7 +178,7 @@ int gemm_small_nt(const void *a, int a_fmt, const void *a_scale, int trans_a, co
     // about square per-XCD tile blocks: group_m = 2^floor(log2(sqrt(tiles / 8)))
     g.group_m = 1;
     while (4 * g.group_m * g.group_m * 8 <= int64_t(g.tiles_m) * g.tiles_n && 2 * g.group_m <= g.tiles_m) g.group_m *= 2;
-    g.aligned_c = ((g.ldc * (c_dtype == PTA_F32 ? 4 : 2)) % 16 == 0) && aligned16(c);
+    g.aligned_c = ((g.ldc * (c_dtype == PTA_F32 ? 4 : 2)) % 16 == 0) && aligned16(g.c);
     switch (sm) {
     case SM_TENSOR: return gemm_small::dispatch_small_tensor(g, akm, bkm, fa, fb, c_dtype, st);
     case SM_ROW: return gemm_small::dispatch_small_row(g, akm, bkm, fa, fb, c_dtype, st);
@@ -176,10 +188,18 @@ int gemm_small_nt(const void *a, int a_fmt, const void *a_scale, int trans_a, co
 }
 } // namespace
 
+// K-contiguous blockwise problems that the small-tile kernel would run on
+// 128 x 128 tiles are faster on the 256 x 256 kernel (2048^3: 24.7 against
+// 31.6 us, 2048 x 2048 x 1024: 15.6 against 19.9; tensorwise and MX are not:
+// 21.3 against 19.7 and 23.9 against 24.5 us at 2048^3).
+static bool block_on_128_tiles(int64_t M, int64_t N, int sm) {
+    return sm == SM_BLOCK && cdiv(M, 128) * cdiv(N, 128) >= PTA_SMALL_T128_MIN;
+}
+
 // Whether pta_gemm_fp8 takes the small-tile kernel: few large tiles, K-major
 // operands with a row stride that is a multiple of 8 (8-byte K-row loads), and
 // every operand offset of the kernel within 32 bits.
-static bool small_path(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b) {
+static bool small_path(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b, int sm) {
     const bool    kmajor = trans_a || !trans_b;
     const int64_t tiles  = cdiv(M, BM) * cdiv(N, BN);
     if (tiles >= (kmajor ? PTA_SMALL_MAX_TILES_KMAJOR : PTA_SMALL_MAX_TILES)) return false;
@@ -187,6 +207,7 @@ static bool small_path(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b
     // and a long K: the large tiles with the K split are faster (blockwise
     // 1024x4096x4096: 62 -> 45 us; at K = 2048 or with fewer tiles they are not)
     if (!kmajor && tiles >= 48 && K >= 4096 && K % 128 == 0) return false;
+    if (!kmajor && block_on_128_tiles(M, N, sm)) return false;
     const int64_t lim = int64_t(1) << 30;
     if (trans_a ? (M % 8 != 0 || (K + 1024) * M >= lim) : 64 * K >= lim) return false;
     if (!trans_b ? (N % 8 != 0 || (K + 1024) * N >= lim) : 64 * K >= lim) return false;
@@ -194,8 +215,8 @@ static bool small_path(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b
 }
 
 extern "C" size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, int trans_a,
-                                              int trans_b, int /*granularity*/) {
-    if (small_path(M, N, K, trans_a, trans_b)) return 0;
+                                              int trans_b, int granularity) {
+    if (small_path(M, N, K, trans_a, trans_b, gran_to_sm(granularity))) return 0;
     size_t ws = 0;
     if (trans_a) ws += static_cast<size_t>(cdiv(M * K, 256) * 256);
     if (!trans_b) ws += static_cast<size_t>(cdiv(N * K, 256) * 256);
@@ -233,7 +254,7 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
     const size_t need = pta_gemm_fp8_workspace_size(M, N, K, trans_a, trans_b, granularity);
     PTA_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                   "workspace of %zu bytes required", need);
-    if (small_path(M, N, K, trans_a, trans_b))
+    if (small_path(M, N, K, trans_a, trans_b, sm))
         return gemm_small_nt(a, a_fmt, a_scale, trans_a, b, b_fmt, b_scale, trans_b, c, c_dtype, trans_c, M, N, K,
                              sm, st);
 
@@ -283,13 +304,32 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
                           b_scale, sb_m, sb_k, sb_bytes, a_scale, sa_m, sa_k, sa_bytes, st, split_ws);
 }
 
-extern "C" int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt,
-                                       int64_t ldb, void *c, int c_dtype, int64_t ldc, int64_t M,
-                                       int64_t N, int64_t K, int granularity, const void *a_scale,
-                                       int64_t sa_m, int64_t sa_k, int a_scale_2d,
-                                       int64_t a_scale_bytes, const void *b_scale, int64_t sb_m,
-                                       int64_t sb_k, int b_scale_2d, int64_t b_scale_bytes,
-                                       pta_stream_t stream) {
+// Whether the kernel-choosing strided entry takes the small-tile kernel: the
+// NT rule of small_path, with the operands' row strides (and the scale
+// extents) in 32-bit reach of the small kernel's buffer offsets.
+static bool strided_small_path(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t sa_bytes,
+                               int64_t sb_bytes, int sm) {
+    const int64_t tiles = cdiv(M, BM) * cdiv(N, BN);
+    if (tiles >= PTA_SMALL_MAX_TILES) return false;
+    if (tiles >= 48 && K >= 4096 && K % 128 == 0) return false; // the K split is faster there
+    if (block_on_128_tiles(M, N, sm)) return false;
+    const int64_t lim = int64_t(1) << 30;
+    return 64 * lda < lim && 64 * ldb < lim && sa_bytes < 2 * lim && sb_bytes < 2 * lim;
+}
+
+static size_t strided_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t sa_bytes,
+                               int64_t sb_bytes, int sm) {
+    if (strided_small_path(M, N, K, lda, ldb, sa_bytes, sb_bytes, sm)) return 0;
+    return static_cast<size_t>(split_ws_bytes(split_tiles(cdiv(M, BM) * cdiv(N, BN), K, device_cu_count())));
+}
+
+// choose: pick the small-tile kernel or the K split as pta_gemm_fp8 does
+// (workspace of strided_ws_bytes); otherwise always the 256 x 256 kernel.
+static int nt_strided(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt, int64_t ldb, void *c,
+                      int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K, int granularity,
+                      const void *a_scale, int64_t sa_m, int64_t sa_k, int a_scale_2d, int64_t a_scale_bytes,
+                      const void *b_scale, int64_t sb_m, int64_t sb_k, int b_scale_2d, int64_t b_scale_bytes,
+                      bool choose, void *workspace, size_t workspace_bytes, pta_stream_t stream) {
     clear_error();
     const int sm = gran_to_sm(granularity);
     PTA_CHECK_ARG(sm >= 0, "unknown granularity %d", granularity);
@@ -315,7 +355,58 @@ extern "C" int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, co
         PTA_CHECK_ARG(K != 0 || M == 0 || N == 0, "K == 0 is not supported by the strided entry");
         return PTA_OK;
     }
+    hipStream_t st       = as_stream(stream);
+    uint8_t    *split_ws = nullptr;
+    if (choose) {
+        const size_t need = strided_ws_bytes(M, N, K, lda, ldb, a_scale_bytes, b_scale_bytes, sm);
+        PTA_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                      "workspace of %zu bytes required", need);
+        if (strided_small_path(M, N, K, lda, ldb, a_scale_bytes, b_scale_bytes, sm)) {
+            gemm_small::SmallArgs g{};
+            g.a = static_cast<const uint8_t *>(a); g.b = static_cast<const uint8_t *>(b); g.c = c;
+            g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
+            g.sa = a_scale; g.sb = b_scale; g.sa_m = sa_m; g.sa_k = sa_k; g.sb_m = sb_m; g.sb_k = sb_k;
+            g.sa_bytes = a_scale_bytes; g.sb_bytes = b_scale_bytes;
+            g.a2d = a_scale_2d != 0; g.b2d = b_scale_2d != 0;
+            if (sm == SM_MX) { // row-major exponents unless a K-block stride is given
+                if (g.sa_k == 0) g.sa_k = 4;
+                if (g.sb_k == 0) g.sb_k = 4;
+            }
+            return small_dispatch(g, false, false, a_fmt, b_fmt, c_dtype, sm, st);
+        }
+        if (need > 0) split_ws = static_cast<uint8_t *>(workspace);
+    }
     return gemm_nt_launch(static_cast<const uint8_t *>(a), a_fmt, lda, static_cast<const uint8_t *>(b), b_fmt,
                           ldb, c, c_dtype, ldc, M, N, K, sm, a_scale_2d != 0, b_scale_2d != 0, a_scale, sa_m,
-                          sa_k, a_scale_bytes, b_scale, sb_m, sb_k, b_scale_bytes, as_stream(stream));
+                          sa_k, a_scale_bytes, b_scale, sb_m, sb_k, b_scale_bytes, st, split_ws);
+}
+
+extern "C" int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt,
+                                       int64_t ldb, void *c, int c_dtype, int64_t ldc, int64_t M,
+                                       int64_t N, int64_t K, int granularity, const void *a_scale,
+                                       int64_t sa_m, int64_t sa_k, int a_scale_2d,
+                                       int64_t a_scale_bytes, const void *b_scale, int64_t sb_m,
+                                       int64_t sb_k, int b_scale_2d, int64_t b_scale_bytes,
+                                       pta_stream_t stream) {
+    return nt_strided(a, a_fmt, lda, b, b_fmt, ldb, c, c_dtype, ldc, M, N, K, granularity, a_scale, sa_m, sa_k,
+                      a_scale_2d, a_scale_bytes, b_scale, sb_m, sb_k, b_scale_2d, b_scale_bytes, false, nullptr,
+                      0, stream);
+}
+
+extern "C" size_t pta_gemm_fp8_nt_strided_ws_size(int64_t M, int64_t N, int64_t K, int granularity, int64_t lda,
+                                                  int64_t ldb, int64_t a_scale_bytes, int64_t b_scale_bytes) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return strided_ws_bytes(M, N, K, lda, ldb, a_scale_bytes, b_scale_bytes, gran_to_sm(granularity));
+}
+
+extern "C" int pta_gemm_fp8_nt_strided_ws(const void *a, int a_fmt, int64_t lda, const void *b, int b_fmt,
+                                          int64_t ldb, void *c, int c_dtype, int64_t ldc, int64_t M,
+                                          int64_t N, int64_t K, int granularity, const void *a_scale,
+                                          int64_t sa_m, int64_t sa_k, int a_scale_2d,
+                                          int64_t a_scale_bytes, const void *b_scale, int64_t sb_m,
+                                          int64_t sb_k, int b_scale_2d, int64_t b_scale_bytes,
+                                          void *workspace, size_t workspace_bytes, pta_stream_t stream) {
+    return nt_strided(a, a_fmt, lda, b, b_fmt, ldb, c, c_dtype, ldc, M, N, K, granularity, a_scale, sa_m, sa_k,
+                      a_scale_2d, a_scale_bytes, b_scale, sb_m, sb_k, b_scale_2d, b_scale_bytes, true, workspace,
+                      workspace_bytes, stream);
 }

@@ -258,7 +258,7 @@ __device__ __forceinline__ int64_t find_tile_group(const int64_t *offs, int64_t 
 template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT, bool PERSIST>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) {
     using CF = TileCfg<BNT>;
-    constexpr int BN_ = CF::BN_, WTN_ = CF::WTN_, TN_ = CF::TN_, TILE_B_ = CF::TILE_B_, STAGE_ = CF::STAGE_;
+    constexpr int BN_ = CF::BN_, WTN_ = CF::WTN_, TN_ = CF::TN_, STAGE_ = CF::STAGE_;
     constexpr int SSLOT_ = CF::SSLOT_, SBASE_ = CF::SBASE_, EPITCH_ = CF::EPITCH_;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // LDS byte address of the dynamic shared buffer (M0 operand of the DMA)

@@ -64,6 +64,12 @@ SIGNATURES = {
         [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i64, _i64, _i64, _i64, _i32,
          _vp, _i64, _i64, _i32, _i64, _vp, _i64, _i64, _i32, _i64, _vp],
     ),
+    "pta_gemm_fp8_nt_strided_ws_size": (_sz, [_i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64]),
+    "pta_gemm_fp8_nt_strided_ws": (
+        _i32,
+        [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i64, _i64, _i64, _i64, _i32,
+         _vp, _i64, _i64, _i32, _i64, _vp, _i64, _i64, _i32, _i64, _vp, _sz, _vp],
+    ),
     "pta_grouped_gemm_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32]),
     "pta_grouped_gemm_fp8": (
         _i32,

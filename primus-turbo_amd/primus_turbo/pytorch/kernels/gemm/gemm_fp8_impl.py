@@ -102,12 +102,16 @@ def gemm_fp8_nt(
     b_scale_2d: bool = False,
     out: torch.Tensor = None,
     K: int = None,
+    large_tiles_only: bool = False,
 ) -> torch.Tensor:
     """C[M, N] = A[M, K] . B[N, K]^T with explicit scale addressing.
 
     Blockwise scales are read as scale[r * stride_r + kb * stride_k] with
     r the row (or row // 128 for a 2-D operand) and kb = k // 128.  K defaults
-    to A's width; B may be wider (zero-padded copies).
+    to A's width; B may be wider (zero-padded copies).  The kernel is chosen
+    as for ``gemm_fp8_impl`` (small-tile kernel for few 256 x 256 tiles, K
+    split for up to half a round of them); ``large_tiles_only`` runs the
+    256 x 256 kernel whatever the shape (same bits as the small-tile kernel).
     """
     gran = _gran_code(granularity)
     assert a.dim() == 2 and b.dim() == 2
@@ -123,10 +127,15 @@ def gemm_fp8_nt(
     sb, sb_bytes = _strided_scale_arg(b_scale, gran)
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=a.device)
-    _C.call(
-        "pta_gemm_fp8_nt_strided", _C.ptr(a), _C.fp8_code(a.dtype), a.stride(0), _C.ptr(b), _C.fp8_code(b.dtype),
-        b.stride(0), _C.ptr(out), _C.out_dtype_code(out.dtype), out.stride(0), M, N, K, gran, _C.ptr(sa),
-        sa_strides[0], sa_strides[1], int(a_scale_2d), sa_bytes, _C.ptr(sb), sb_strides[0],
-        sb_strides[1], int(b_scale_2d), sb_bytes, _C.stream(a.device),
+    args = (
+        _C.ptr(a), _C.fp8_code(a.dtype), a.stride(0), _C.ptr(b), _C.fp8_code(b.dtype), b.stride(0), _C.ptr(out),
+        _C.out_dtype_code(out.dtype), out.stride(0), M, N, K, gran, _C.ptr(sa), sa_strides[0], sa_strides[1],
+        int(a_scale_2d), sa_bytes, _C.ptr(sb), sb_strides[0], sb_strides[1], int(b_scale_2d), sb_bytes,
     )
+    if large_tiles_only:
+        _C.call("pta_gemm_fp8_nt_strided", *args, _C.stream(a.device))
+        return out
+    ws_n = _C.query("pta_gemm_fp8_nt_strided_ws_size", M, N, K, gran, a.stride(0), b.stride(0), sa_bytes, sb_bytes)
+    ws = _C.workspace(ws_n, a.device)
+    _C.call("pta_gemm_fp8_nt_strided_ws", *args, _C.ptr(ws), 0 if ws is None else ws.numel(), _C.stream(a.device))
     return out

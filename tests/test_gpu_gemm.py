@@ -110,11 +110,11 @@ def test_gemm_blockwise_vs_oracle(mnk, layout, qdt):
     _check(out, ref, f"BLOCKWISE {layout}")
 
 
-@pytest.mark.parametrize("mnk", [(2304, 3072, 2048), (2300, 3000, 1024), (4096, 2048, 7168), (2048, 4352, 1152), (1024, 4096, 4096)])
+@pytest.mark.parametrize("mnk", [(2304, 3072, 4096), (2300, 3000, 4096), (4096, 2048, 7168), (2048, 4352, 4224), (1024, 4096, 4096)])
 @pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
 def test_gemm_k_split_vs_oracle(mnk, gran):
-    """Problems of 72-128 tiles of 256 x 256 with K >= 1024 (from 48 tiles with
-    K >= 4096 and K-contiguous operands) run every tile as two half-K
+    """Problems of 48-128 tiles of 256 x 256 with K >= 4096 (K-contiguous
+    operands; an odd count of K blocks included) run every tile as two half-K
     workgroups (fp32 partials handed over through the workspace), including
     partial edge tiles: the result meets the oracle criterion and
     matches the unsplit strided entry (same operands) to within fp32 summation
@@ -151,7 +151,7 @@ def test_gemm_k_split_vs_oracle(mnk, gran):
         nt = dict(a_scale=sa, sa_strides=_mx_strides(sa), b_scale=sb, sb_strides=_mx_strides(sb))
     out = gemm_fp8_impl(qa, sa, False, qb, sb, True, torch.bfloat16, False, g.value)
     again = gemm_fp8_impl(qa, sa, False, qb, sb, True, torch.bfloat16, False, g.value)
-    whole = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt)[:, :N]
+    whole = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt, large_tiles_only=True)[:, :N]
     ref = O.gemm_ref(da, db, False, True)
     _check(out, ref, f"{gran} split")
     assert torch.equal(out, again), "split GEMM is not deterministic"
@@ -168,7 +168,7 @@ def test_gemm_k_split_out_dtype_trans_c(gran, out_dtype, trans_c):
     the oracle criterion on a 108-tile problem with a partial edge tile."""
     turbo, _, _, _, SG, SR, gemm_fp8_impl = _mods()
     g = getattr(SG, gran)
-    M, N, K = 2300, 3000, 2048
+    M, N, K = 2300, 3000, 4096
     qdt = torch.float8_e4m3fn
     a = randn((M, K), seed=31, outliers=0.001).cuda()
     b = randn((N, K), seed=32, outliers=0.001).cuda()

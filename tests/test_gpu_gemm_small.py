@@ -84,12 +84,12 @@ def _case(M, N, K, layout, trans_c, gran_name, fa=E4, fb=E4, out_dtype=torch.bfl
         nt = dict(a_scale=sa, sa_strides=(K // 32, 4), b_scale=sb, sb_strides=(K // 32, 4))
     out = gemm_fp8_impl(qa, sa, ta, qb, sb, tb, out_dtype, trans_c, g.value)
     if not trans_c:
-        ref = gemm_fp8_nt(a_nt, b_nt, out_dtype, g, **nt)
+        ref = gemm_fp8_nt(a_nt, b_nt, out_dtype, g, **nt, large_tiles_only=True)
     else:  # C^T = B' A'^T: exchange the operands and their scale addressing
         other = {"a_scale": "b_scale", "sa_strides": "sb_strides", "a_scale_2d": "b_scale_2d"}
         other.update({v: k for k, v in other.items()})
         sw = {other[k]: v for k, v in nt.items()}
-        ref = gemm_fp8_nt(b_nt, a_nt, out_dtype, g, **sw)
+        ref = gemm_fp8_nt(b_nt, a_nt, out_dtype, g, **sw, large_tiles_only=True)
     torch.cuda.synchronize()
     assert out.shape == ref.shape
     diff = (out.view(torch.int16 if out.element_size() == 2 else torch.int32)
@@ -129,3 +129,68 @@ def test_small_path_mx_matches_large_tile_kernel(mnk, trans_c):
 def test_small_path_formats_and_outputs(fmts, out_dtype, gran, mnk):
     layout = "NT" if gran == "MX_BLOCKWISE" else "NN"
     _case(*mnk, layout, False, gran, fmts[0], fmts[1], out_dtype)
+
+
+def _strided_args(M, N, K, scales, seed):
+    """Operands as row-strided views (row stride K + 64) with scales in one of
+    the layouts the autograd functions hand to gemm_fp8_nt."""
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity as SG
+
+    qa = _fp8((M, K + 64), E4, seed)[:, :K]
+    qb = _fp8((N, K + 64), E4, seed + 1)[:, :K]
+    kb = _cd(K, 128)
+    if scales == "TENSORWISE":
+        return qa, qb, SG.TENSORWISE, dict(a_scale=_scales((1,), seed + 2), b_scale=_scales((1,), seed + 3))
+    if scales == "ROWWISE":
+        return qa, qb, SG.ROWWISE, dict(a_scale=_scales((M,), seed + 2), b_scale=_scales((N,), seed + 3))
+    if scales == "BLOCK_1Dx2D":  # forward: A [M, K/128], B [N/128, K/128]
+        return qa, qb, SG.BLOCKWISE, dict(a_scale=_scales((M, kb), seed + 2), sa_strides=(kb, 1),
+                                          b_scale=_scales((_cd(N, 128), kb), seed + 3), sb_strides=(kb, 1),
+                                          b_scale_2d=True)
+    if scales == "BLOCK_1Dx1D":  # wgrad: both K-block major [K/128, rows]
+        return qa, qb, SG.BLOCKWISE, dict(a_scale=_scales((kb, M), seed + 2), sa_strides=(1, M),
+                                          b_scale=_scales((kb, N), seed + 3), sb_strides=(1, N))
+    if scales == "MX_ROWMAJOR":  # [rows, K/32] bytes
+        return qa, qb, SG.MX_BLOCKWISE, dict(a_scale=_exps((M, K // 32), seed + 2), sa_strides=(K // 32, 4),
+                                             b_scale=_exps((N, K // 32), seed + 3), sb_strides=(K // 32, 4))
+    # MX_KMAJOR: [K/128, rows, 4] bytes
+    return qa, qb, SG.MX_BLOCKWISE, dict(a_scale=_exps((K // 128, M, 4), seed + 2), sa_strides=(4, 4 * M),
+                                         b_scale=_exps((K // 128, N, 4), seed + 3), sb_strides=(4, 4 * N))
+
+
+@pytest.mark.parametrize("scales", ["TENSORWISE", "ROWWISE", "BLOCK_1Dx2D", "BLOCK_1Dx1D", "MX_ROWMAJOR", "MX_KMAJOR"])
+@pytest.mark.parametrize("mnk", [(512, 1024, 1024), (200, 136, 1024), (1904, 2000, 256)])
+def test_strided_entry_small_kernel_matches_large(scales, mnk):
+    """gemm_fp8_nt (the autograd functions' NT entry) takes the small-tile kernel
+    for few 256 x 256 tiles (blockwise ones it would run on 128 x 128 tiles
+    excepted): row-strided operands, a row-strided output and each scale
+    layout give the same bits as the 256 x 256 kernel."""
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_nt
+
+    M, N, K = mnk
+    qa, qb, g, nt = _strided_args(M, N, K, scales, 40)
+    wide = torch.zeros((M, N + 24), dtype=torch.bfloat16, device="cuda")
+    out = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt, out=wide[:, :N])
+    ref = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt, large_tiles_only=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"{int((out != ref).sum())} outputs differ"
+    assert not wide[:, N:].float().any(), "columns past N of the output rows were written"
+
+
+@pytest.mark.parametrize("scales", ["TENSORWISE", "BLOCK_1Dx2D", "BLOCK_1Dx1D", "MX_KMAJOR"])
+def test_strided_entry_k_split(scales):
+    """108 tiles of 256 x 256 with K = 4096: gemm_fp8_nt runs the K split
+    through its workspace; the result matches the unsplit kernel to within fp32
+    summation order and repeats bit for bit."""
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_nt
+
+    M, N, K = 2300, 3000, 4096
+    qa, qb, g, nt = _strided_args(M, N, K, scales, 50)
+    out = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt)
+    again = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt)
+    ref = gemm_fp8_nt(qa, qb, torch.bfloat16, g, **nt, large_tiles_only=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), "split GEMM is not deterministic"
+    o, r = out.double(), ref.double()
+    assert torch.isfinite(o).all()
+    assert float((o - r).abs().max()) <= 2.0 ** -6 * float(r.abs().max()), "split and whole results differ beyond rounding"
