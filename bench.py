@@ -183,6 +183,78 @@ def _accuracy(seed_inputs, gpu_out):
             "reference": "fp64 product of the dequantized FP8 operands (CPU oracle), whole output"}
 
 
+def _stream_ceiling(args):
+    """Each BASELINE quantize kernel next to the streaming probe (pta_stream_probe)
+    at the same bytes: "copy" when the kernel writes about what it reads, "read 2
+    write 1" for a cast; the faster of plain and non-temporal accesses.
+    Both are timed the same way (settled clock, the same buffers every call), in
+    one process; the probe's rate is the ceiling the kernel is compared with."""
+    import torch
+
+    from primus_turbo.pytorch import _C
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_dual_impl,
+        quant_fp8_blockwise_for_weight_impl,
+        quant_fp8_blockwise_segment_m_row_col_impl,
+        quantize_fp8_rowwise_impl,
+        quantize_mxfp8_impl,
+    )
+
+    e4 = torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(4)
+    dev = "cuda"
+    it = max(10, args.steps // 2)
+
+    def rnd(shape):
+        return torch.randn(shape, generator=g).bfloat16().to(dev)
+
+    lens = _zipf_counts(65536, 32, 28, 0).to(dev)
+    offs = group_offs_from_lens(lens)
+    cases = [
+        ("act dual 1x128 + transposed column copy (config 3 / headline)", (4096, 7168),
+         lambda x: quant_fp8_blockwise_dual_impl(x, e4, 128, col_transposed=True, row_scale_kmajor=True)),
+        ("weight 128x128 (headline)", (18432, 7168), lambda x: quant_fp8_blockwise_for_weight_impl(x, e4, 128)),
+        ("rowwise (config 2)", (8192, 4096), lambda x: quantize_fp8_rowwise_impl(x, e4, -1)),
+        ("weight 128x128, 32 experts (config 4)", (32, 2048, 7168),
+         lambda x: quant_fp8_blockwise_for_weight_impl(x, e4, 128)),
+        ("grouped segment row + col (config 4)", (65536, 7168),
+         lambda x: quant_fp8_blockwise_segment_m_row_col_impl(x, e4, 128, lens, offs)),
+        ("MX dual, k-major exponents (config 5)", (8192, 8192),
+         lambda x: quantize_mxfp8_impl(x, e4, None, 32, with_trans=True, exp_kmajor=True)),
+    ]
+    out = []
+    for name, shape, fn in cases:
+        x = rnd(shape)
+        res = fn(x)
+        res = res if isinstance(res, (tuple, list)) else (res,)
+        rd = x.numel() * x.element_size()
+        wr = sum(t.numel() * t.element_size() for t in res if isinstance(t, torch.Tensor) and t.device.type == "cuda")
+        q_ms = _time_settled(lambda: fn(x), it)
+        del res
+        ratio = 2 if wr < 0.6 * rd else 1
+        wb = (wr if ratio == 2 else (rd + wr) // 2) // 16 * 16
+        src = torch.empty(ratio * wb, dtype=torch.uint8, device=dev).random_(0, 255)
+        dst = torch.empty(wb, dtype=torch.uint8, device=dev)
+        p_ms, nt = None, 0
+        for nt_try in (0, 1):  # the faster of plain and non-temporal accesses is the ceiling
+            probe = lambda: _C.call("pta_stream_probe", _C.ptr(src), _C.ptr(dst), wb, ratio, nt_try,  # noqa: E731
+                                    _C.stream(src.device))
+            t = _time_settled(probe, it)
+            if p_ms is None or t < p_ms:
+                p_ms, nt = t, nt_try
+        q_tbs = (rd + wr) / (q_ms * 1e-3) / 1e12
+        p_tbs = (ratio + 1) * wb / (p_ms * 1e-3) / 1e12
+        out.append({"kernel": name, "shape": list(shape), "read_MB": round(rd / 1e6, 1), "write_MB": round(wr / 1e6, 1),
+                    "kernel_us": round(q_ms * 1e3, 1), "kernel_TBps": round(q_tbs, 2),
+                    "probe": ("read 2 write 1" if ratio == 2 else "copy") + (", non-temporal" if nt else ""),
+                    "probe_us": round(p_ms * 1e3, 1), "probe_TBps": round(p_tbs, 2),
+                    "kernel_frac_of_probe": round(q_tbs / p_tbs, 3), "kernel_frac_of_hbm": round(q_tbs / 8.0, 3)})
+        del x, src, dst
+        torch.cuda.empty_cache()
+    print(json.dumps({"stream_ceiling": out, "hbm_peak_TBps": 8.0}))
+
+
 def _quant_calls(a, w):
     """Three calls of each BASELINE quantize kernel on its config's shape, for
     the FETCH_SIZE / WRITE_SIZE counter passes (no timing)."""
@@ -231,12 +303,17 @@ def main():
                          "BASELINE quantize kernel (both for counter passes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with three 256 MiB device copies (reference for the FETCH/WRITE counters)")
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="only: each BASELINE quantize kernel next to a plain streaming kernel of the same bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the FP8 linear path is benchmarked on a "
                                    "single MI355X (multi-GPU sharding is a design note, not a run)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.stream_ceiling:
+        _stream_ceiling(args)
+        return
 
     import torch
 

@@ -64,6 +64,7 @@ SIGNATURES = {
         [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i64, _i64, _i64, _i64, _i32,
          _vp, _i64, _i64, _i32, _i64, _vp, _i64, _i64, _i32, _i64, _vp],
     ),
+    "pta_stream_probe": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp]),
     "pta_gemm_fp8_nt_strided_ws_size": (_sz, [_i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64]),
     "pta_gemm_fp8_nt_strided_ws": (
         _i32,
