@@ -70,6 +70,29 @@ def test_workspace_queries():
     assert _C.query("pta_gemm_fp8_workspace_size", 4096, 4096, 512, 0, 0, 0) >= 4096 * 512
     assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 4, 100, 1) == 0
     assert _C.query("pta_quantize_fp8_rowwise_workspace_size", 1, 100, 64) > 0
+    # the K split: at most half a round of 256 x 256 tiles with K >= 4096 (one
+    # fp32 256 x 256 partial tile per split tile); shorter K runs whole
+    split = 256 * 256 * 4
+    assert _C.query("pta_gemm_fp8_workspace_size", 2304, 3072, 4096, 0, 1, 1) >= 108 * split
+    assert _C.query("pta_gemm_fp8_workspace_size", 2304, 3072, 2048, 0, 1, 1) == 0
+    assert _C.query("pta_gemm_fp8_workspace_size", 4096, 18432, 7168, 0, 1, 3) == 0
+
+
+def test_strided_entry_workspace_queries():
+    """pta_gemm_fp8_nt_strided_ws_size(M, N, K, granularity, lda, ldb, sa_bytes,
+    sb_bytes): 0 where the small-tile kernel or the whole 256 x 256 kernel runs,
+    the split partials where the K split does (host-side rules, no GPU)."""
+    from primus_turbo.pytorch import _C
+
+    q = lambda *a: _C.query("pta_gemm_fp8_nt_strided_ws_size", *a)  # noqa: E731
+    assert q(512, 1024, 1024, 1, 1024, 1024, 4, 4) == 0        # 8 tiles: small-tile kernel
+    assert q(2048, 2048, 2048, 3, 2048, 2048, 4 << 20, 4 << 20) == 0  # blockwise on 128x128 tiles: whole
+    assert q(2048, 2048, 2048, 1, 2048, 2048, 4, 4) == 0       # tensorwise: small-tile kernel
+    assert q(2304, 3072, 2048, 3, 2048, 2048, 1 << 20, 1 << 20) == 0  # 108 tiles, K < 4096: whole
+    assert q(2304, 3072, 4096, 3, 4096, 4096, 1 << 20, 1 << 20) >= 108 * 256 * 256 * 4  # K split
+    assert q(1024, 4096, 4096, 4, 4096, 4096, 1 << 20, 1 << 20) >= 64 * 256 * 256 * 4   # 64 tiles, K >= 4096
+    assert q(4096, 18432, 7168, 3, 7168, 7168, 1 << 20, 1 << 20) == 0  # the headline: whole tiles
+    assert q(0, 1024, 1024, 1, 1024, 1024, 4, 4) == 0
 
 
 def test_argument_errors_of_the_grouped_and_moe_entries():
