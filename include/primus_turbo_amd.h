@@ -274,9 +274,10 @@ int pta_grouped_compute_padded_offs(const int64_t *offs, int64_t *padded_offs, i
  *   TN: A[K,M] a_scale[K/128,M];  B[K,N] b_scale[K/128,N]
  * workspace may be NULL when pta_gemm_fp8_workspace_size() returns 0 for
  * these arguments.  The workspace holds the NN / TN operand transposes and,
- * for problems of at most half a round of 256 x 256 tiles with K >= 4096 and
- * K % 128 == 0, the fp32 partial tiles of the K split (each tile then runs as
- * two half-K workgroups; not under stream capture).  Replaces gemm_fp8_impl
+ * for problems of at most half a round of 256 x 256 tiles with K >= 4096 (at
+ * most a quarter round: K >= 3072) and K % 128 == 0, the fp32 partial tiles of
+ * the K split (each tile then runs as two half-K workgroups; not under stream
+ * capture).  Replaces gemm_fp8_impl
  * (primus_turbo/pytorch/kernels/gemm/gemm_fp8_impl.py:438-467) and the native
  * hipblaslt/ck/turbo_gemm_fp8 ops behind it. */
 size_t pta_gemm_fp8_workspace_size(int64_t M, int64_t N, int64_t K, int trans_a, int trans_b,
@@ -308,7 +309,8 @@ int pta_gemm_fp8_nt_strided(const void *a, int a_fmt, int64_t lda, const void *b
  * fewer than 72 tiles of 256 x 256 run on the small-tile kernel (results bit
  * for bit those of the 256 x 256 kernel; blockwise problems it would run on
  * 128 x 128 tiles stay on the 256 x 256 kernel), and problems of at most half
- * a round of tiles with K >= 4096 and K % 128 == 0 take the K split, whose
+ * a round of tiles with K >= 4096 (a quarter round: K >= 3072) and
+ * K % 128 == 0 take the K split, whose
  * fp32 partial tiles and per-call tags live in the workspace (not under
  * stream capture; two calls in flight must not share one workspace).  The
  * workspace size depends on the shape, the granularity, the row strides and

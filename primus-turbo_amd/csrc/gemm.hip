@@ -25,22 +25,33 @@
 #ifndef PTA_SMALL_FORCE_TILE
 #define PTA_SMALL_FORCE_TILE -1
 #endif
+// Shortest K for the K split of small problems (see split_tiles): up to half
+// a round of tiles, and up to a quarter round.
+#ifndef PTA_SPLIT_MIN_K
+#define PTA_SPLIT_MIN_K 4096
+#endif
+#ifndef PTA_SPLIT_MIN_K_QUARTER
+#define PTA_SPLIT_MIN_K_QUARTER 3072
+#endif
 
 namespace pta {
 using namespace gemm_detail;
 
 // K split for problems of at most half a round of tiles (one 256 x 256 tile
-// per CU and round) and K >= 4096: every tile runs as two half-K workgroups
-// whose fp32 partials meet in the workspace, so twice as many CUs work.  The
-// hand-over (256 KB written and read per tile) costs a fixed ~6-10 us, so a
-// shorter K runs whole (108 tiles, split / whole: K = 2048 1.22-1.27, 3072
-// 1.01-1.04, 4096 0.92-0.98, 6144 0.78-0.80; 64 tiles at K = 4096: 0.78-0.81).
-// Splitting the last round of larger problems measured no faster (headline
+// per CU and round) and K >= 4096, or at most a quarter round and K >= 3072:
+// every tile runs as two half-K workgroups whose fp32 partials meet in the
+// workspace, so twice as many CUs work.  The hand-over (256 KB written and
+// read per tile) costs a fixed ~6-10 us, so a shorter K runs whole
+// (kernel-trace medians, split / whole; 108 tiles: K = 2048 1.22-1.27, 3072
+// 1.01-1.04, 4096 0.92-0.98, 6144 0.78-0.80; 128 tiles: 2048 1.14-1.22, 3072
+// 0.99-1.00; 64 tiles: 2048 1.02-1.03, 3072 0.84, 4096 0.78-0.81).  Splitting
+// the last round of larger problems measured no faster (headline
 // 4096x18432x7168: +1%), so those run whole.  Returns the number of split
 // tiles (0: none).
 int64_t split_tiles(int64_t tiles, int64_t K, int cus) {
-    if (K % BK != 0 || K < 4096 || tiles <= 0 || cus <= 0) return 0;
-    return 2 * tiles <= cus ? tiles : 0;
+    if (K % BK != 0 || tiles <= 0 || cus <= 0 || 2 * tiles > cus) return 0;
+    const int64_t kmin = 4 * tiles <= cus ? PTA_SPLIT_MIN_K_QUARTER : PTA_SPLIT_MIN_K;
+    return K >= kmin ? tiles : 0;
 }
 
 constexpr int64_t SPLIT_TILE_BYTES = int64_t(BM) * BN * 4;

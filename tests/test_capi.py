@@ -91,6 +91,8 @@ def test_strided_entry_workspace_queries():
     assert q(2304, 3072, 2048, 3, 2048, 2048, 1 << 20, 1 << 20) == 0  # 108 tiles, K < 4096: whole
     assert q(2304, 3072, 4096, 3, 4096, 4096, 1 << 20, 1 << 20) >= 108 * 256 * 256 * 4  # K split
     assert q(1024, 4096, 4096, 4, 4096, 4096, 1 << 20, 1 << 20) >= 64 * 256 * 256 * 4   # 64 tiles, K >= 4096
+    assert q(1024, 4096, 3072, 3, 3072, 3072, 1 << 20, 1 << 20) >= 64 * 256 * 256 * 4   # a quarter round: K >= 3072
+    assert q(2304, 3072, 3072, 3, 3072, 3072, 1 << 20, 1 << 20) == 0  # 108 tiles at K = 3072: whole
     assert q(4096, 18432, 7168, 3, 7168, 7168, 1 << 20, 1 << 20) == 0  # the headline: whole tiles
     assert q(0, 1024, 1024, 1, 1024, 1024, 4, 4) == 0
 

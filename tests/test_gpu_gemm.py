@@ -110,11 +110,12 @@ def test_gemm_blockwise_vs_oracle(mnk, layout, qdt):
     _check(out, ref, f"BLOCKWISE {layout}")
 
 
-@pytest.mark.parametrize("mnk", [(2304, 3072, 4096), (2300, 3000, 4096), (4096, 2048, 7168), (2048, 4352, 4224), (1024, 4096, 4096)])
+@pytest.mark.parametrize("mnk", [(2304, 3072, 4096), (2300, 3000, 4096), (4096, 2048, 7168), (2048, 4352, 4224), (1024, 4096, 4096), (1000, 4000, 3072)])
 @pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
 def test_gemm_k_split_vs_oracle(mnk, gran):
-    """Problems of 48-128 tiles of 256 x 256 with K >= 4096 (K-contiguous
-    operands; an odd count of K blocks included) run every tile as two half-K
+    """Problems of 48-128 tiles of 256 x 256 with K >= 4096, or up to 64 tiles
+    with K >= 3072 (blockwise; the others take the small-tile kernel there),
+    K-contiguous operands, an odd count of K blocks included, run every tile as two half-K
     workgroups (fp32 partials handed over through the workspace), including
     partial edge tiles: the result meets the oracle criterion and
     matches the unsplit strided entry (same operands) to within fp32 summation
