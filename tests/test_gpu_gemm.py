@@ -160,6 +160,38 @@ def test_gemm_k_split_vs_oracle(mnk, gran):
     assert np.max(np.abs(o - w)) <= 2.0 ** -6 * np.max(np.abs(w)), "split and whole results differ beyond rounding"
 
 
+def test_gemm_k_split_workspace_reuse():
+    """One workspace for consecutive K-split calls on different activations,
+    enqueued back to back: each call's tag keeps its second halves from
+    adding a partial tile an earlier call left in the workspace, so every
+    output matches the unsplit kernel on its own operands."""
+    turbo, _, _, _, SG, _, _ = _mods()
+    from primus_turbo.pytorch import _C
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_nt
+
+    g = SG.TENSORWISE
+    M, N, K = 1024, 4096, 4096  # 64 tiles, K >= 4096: split
+    ws_n = _C.query("pta_gemm_fp8_workspace_size", M, N, K, 0, 1, g.value)
+    assert ws_n >= 64 * 256 * 256 * 4
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    b = randn((N, K), seed=40).cuda()
+    qb, sb = turbo.ops.quantize_fp8(b, torch.float8_e4m3fn, g)
+    calls = []
+    for seed, amp in ((41, 30.0), (42, 0.01), (43, 1.0)):
+        a = (randn((M, K), seed=seed).float() * amp).bfloat16().cuda()
+        qa, sa = turbo.ops.quantize_fp8(a, torch.float8_e4m3fn, g)
+        calls.append((qa, sa, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
+    for qa, sa, out in calls:
+        _C.call("pta_gemm_fp8", _C.ptr(qa), _C.PTA_E4M3, _C.ptr(sa), 0, _C.ptr(qb), _C.PTA_E4M3, _C.ptr(sb), 1,
+                _C.ptr(out), _C.PTA_BF16, 0, M, N, K, g.value, _C.ptr(ws), ws_n, _C.stream(qa.device))
+    torch.cuda.synchronize()
+    for i, (qa, sa, out) in enumerate(calls):
+        whole = gemm_fp8_nt(qa, qb, torch.bfloat16, g, a_scale=sa, b_scale=sb, large_tiles_only=True)
+        o, w = out.double(), whole.double()
+        assert torch.isfinite(o).all(), f"call {i}: non-finite output"
+        assert float((o - w).abs().max()) <= 2.0 ** -6 * float(w.abs().max()), f"call {i} differs from its own product"
+
+
 @pytest.mark.parametrize("gran", ["TENSORWISE", "BLOCKWISE"])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 @pytest.mark.parametrize("trans_c", [False, True])

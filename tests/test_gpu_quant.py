@@ -91,6 +91,32 @@ def test_tensorwise_single_launch_sizes(n, spike):
     assert_bytes_equal(u8(q), qo, "fp8 bytes")
 
 
+def test_tensorwise_single_launch_workspace_reuse():
+    """One workspace for consecutive single-launch calls on different inputs,
+    enqueued back to back (a larger amax first, then a smaller one, then a
+    smaller n): each call's per-call tag keeps it from reading the partial
+    maxima an earlier call left in the workspace."""
+    from primus_turbo.pytorch import _C
+
+    n = (1 << 20) + 5
+    ws_n = _C.query("pta_quantize_fp8_tensorwise_workspace_size", n)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    cases = []
+    for seed, spike, m in ((31, 900.0, n), (32, 3.0, n), (33, 40.0, n // 3)):
+        x = _input((m,), seed=seed, special=False)
+        x[m // 2] = spike
+        cases.append((x, x.cuda(), torch.empty(m, dtype=torch.uint8, device="cuda"),
+                      torch.empty((), dtype=torch.float32, device="cuda")))
+    for _, xd, q, s in cases:
+        _C.call("pta_quantize_fp8_tensorwise", _C.ptr(xd), _C.PTA_BF16, xd.numel(), None, _C.ptr(q), _C.PTA_E4M3,
+                _C.ptr(s), _C.ptr(ws), ws_n, _C.stream(xd.device))
+    torch.cuda.synchronize()
+    for i, (x, _, q, s) in enumerate(cases):
+        qo, so = O.quant_tensorwise(x, FMT[torch.float8_e4m3fn])
+        assert_f32_bitexact(f32(s), so, f"scale_inv of call {i}")
+        assert_bytes_equal(u8(q), qo, f"fp8 bytes of call {i}")
+
+
 @pytest.mark.parametrize("n", [1, 4096, 1 << 20, (1 << 20) + 13])
 @pytest.mark.parametrize("qdt", FP8)
 def test_tensorwise_vs_reference_kernels(n, qdt):
