@@ -273,6 +273,16 @@ def _autograd_case(m, n, k, layout, fmt_name, gran_name, block_size=None, dtype=
         assert s > thr, f"{name} SNR {s:.1f} dB <= {thr}"
 
 
+@pytest.mark.parametrize("mnk", [(1024, 4096, 4096), (2272, 3008, 4096)])
+@pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
+def test_gemm_fp8_autograd_k_split_shapes(mnk, gran):
+    """A layer whose forward and dgrad GEMMs take the K split (64 / 108 tiles
+    of 256 x 256, K = 4096; the second with partial edge tiles) meets the
+    reference's end-to-end criterion for C, dA and dB."""
+    bs = {"BLOCKWISE": 128, "MX_BLOCKWISE": 32}.get(gran)
+    _autograd_case(*mnk, "NT", "E4M3", gran, block_size=bs)
+
+
 @pytest.mark.parametrize("m", [255, 512])
 @pytest.mark.parametrize("n,k", [(512, 576), (1024, 256)])
 @pytest.mark.parametrize("layout", ["NT", "NN"])
