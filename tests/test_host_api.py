@@ -148,3 +148,25 @@ def test_quantized_tensor_view_autograd():
     g = torch.ones((128, 128), dtype=torch.bfloat16)
     (gin,) = torch.autograd.grad(v, qt, g)
     assert gin.shape == (64, 256)
+
+
+@pytest.mark.parametrize("gran", ["TENSORWISE", "ROWWISE", "BLOCKWISE", "MX_BLOCKWISE"])
+def test_dense_gemm_fp8_refuses_graph_capture(monkeypatch, gran):
+    """Dense gemm_fp8 raises RuntimeError under HIP graph capture before it
+    touches the device (the capture state is forced from the host here)."""
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import Float8QuantConfig, ScaleDtype, ScalingGranularity
+
+    g = getattr(ScalingGranularity, gran)
+    kw = {}
+    if g == ScalingGranularity.BLOCKWISE:
+        kw = dict(block_size=128)
+    elif g == ScalingGranularity.MX_BLOCKWISE:
+        kw = dict(block_size=32, scale_dtype=ScaleDtype.E8M0)
+    cfg = Float8QuantConfig(granularity=g, **kw)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    a = torch.zeros(128, 128, dtype=torch.bfloat16)
+    b = torch.zeros(128, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        turbo.ops.gemm_fp8(a, b, trans_b=True, config=cfg)
