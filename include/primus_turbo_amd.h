@@ -452,15 +452,6 @@ int pta_moe_unpermute(const void *permuted, int64_t num_permuted, int dtype, int
                       const float *permuted_probs, float *probs, int probs_stride,
                       pta_stream_t stream);
 
-/* Measurement helper, no counterpart in the reference: streams write_bytes
- * (a multiple of 16) into dst while reading read_ratio * write_bytes from src
- * (read_ratio 1: a copy; 2: two 16-byte loads folded into each 16-byte store,
- * the byte pattern of a bf16 -> fp8 cast), 16-byte accesses, several loads in
- * flight per lane, non-temporal when nontemporal != 0.  bench.py times it at
- * the quantize kernels' byte counts: the ceiling they are compared with. */
-int pta_stream_probe(const void *src, void *dst, int64_t write_bytes, int read_ratio, int nontemporal,
-                     pta_stream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

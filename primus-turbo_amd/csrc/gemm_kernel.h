@@ -430,7 +430,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
             // one dword (four 32-K exponents) per row, staged by the operand
             // DMA waves: 64 A rows and 64 B rows each (all eight waves staging
             // one block each measured 8-10% slower: it puts a DMA back into
-            // the other wave of every SIMD)
+            // the other wave of every SIMD).  The four DMA waves cover the
+            // B exponents of a 256-column tile exactly (slots 4-7).
+            static_assert(BN_ == 256, "MX exponent staging assumes four 64-row B slots");
             if (dma_wave) {
                 dma4(lds0 + SBASE_ + stage * SSLOT_ + (wave & 3) * 256, mx_voa, dMXA,
                      static_cast<int>(kb + kb_base) * mx_ksa);

@@ -64,7 +64,6 @@ SIGNATURES = {
         [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i64, _i64, _i64, _i64, _i32,
          _vp, _i64, _i64, _i32, _i64, _vp, _i64, _i64, _i32, _i64, _vp],
     ),
-    "pta_stream_probe": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp]),
     "pta_gemm_fp8_nt_strided_ws_size": (_sz, [_i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64]),
     "pta_gemm_fp8_nt_strided_ws": (
         _i32,
@@ -151,8 +150,10 @@ def call(name: str, *args) -> None:
 
 
 def query(name: str, *args) -> int:
-    """A size query (a pure function of its integer arguments; answers are cached)."""
-    key = (name, args)
+    """A size query.  Answers are cached per (entry, arguments, current device):
+    some sizes depend on the device as well (the GEMM workspaces hold the K
+    split's partial tiles, whose use depends on the device's CU count)."""
+    key = (name, args, torch.cuda.current_device() if _gpu_checked else -1)
     v = _queries.get(key)
     if v is None:
         if len(_queries) >= 4096:  # shapes that vary per call (token counts) must not grow it forever

@@ -112,8 +112,10 @@ def grouped_gemm_fp8_variable_k_impl(
         # a 128-row scale block of a [M_total/128, OUT] column scale must not
         # straddle two groups: the kernel indexes scale rows by padded segment
         # offset / 128, which is only the quantizer's row when the offsets are
-        # 128-aligned (the segment quant's vk_offs are).  One host read.
-        if bool(torch.any(group_offs.to(torch.int64) % 128 != 0).item()):
+        # 128-aligned (the segment quant's vk_offs are).  One host read, left
+        # out under stream capture (no host read may happen there).
+        if not torch.cuda.is_current_stream_capturing() and bool(
+                torch.any(group_offs.to(torch.int64) % 128 != 0).item()):
             raise RuntimeError("variable-K BLOCKWISE grouped GEMM needs 128-aligned group offsets "
                                "(the segment quant's padded offsets)")
     a = a.contiguous()
