@@ -55,6 +55,31 @@ const char *pta_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int pta_abi_version(void);
 
+/* Bounded cross-workgroup waits.  Two kernels hand data from one workgroup to
+ * another through the caller's workspace: the single-launch tensorwise
+ * quantize (pta_quantize_fp8_tensorwise and _noalloc, up to 2^21 elements,
+ * not under stream capture: every workgroup waits for all others' partial
+ * maxima) and the K split of the dense GEMM (pta_gemm_fp8 and
+ * pta_gemm_fp8_nt_strided_ws: the second half of a tile waits for the
+ * first).  Each wait is bounded: if it gives up (some workgroups could not
+ * start, e.g. because concurrent work on other streams held the CUs), the
+ * affected outputs become NaN and the kernel writes the call's 64-bit tag
+ * into a status word of the workspace.  No counterpart in the reference.
+ *
+ * pta_last_wait_status: for the last entry-point call made on this host
+ * thread, *tag = that call's tag and *status_offset = the status word's byte
+ * offset in the workspace it was given (8-byte aligned), or -1 when that call
+ * launched no bounded wait.  After the stream has finished the call, the
+ * uint64 at workspace + *status_offset equals *tag if and only if a wait gave
+ * up.  (The workspace is not cleared: any other value means success.) */
+int pta_last_wait_status(uint64_t *tag, int64_t *status_offset);
+/* Test hook, no counterpart in the reference: on != 0 makes every bounded
+ * wait launched from now on (any thread) poll for a tag that is never
+ * published, with a short limit, so each one gives up quickly and every
+ * kernel still exits; 0 restores normal waits.  For tests of the give-up
+ * path only. */
+void pta_test_force_wait_giveup(int on);
+
 /* ============================================================================
  * Quantization
  * ========================================================================== */

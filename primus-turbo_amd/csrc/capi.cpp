@@ -19,7 +19,25 @@ void set_error(const char *fmt, ...) {
     va_end(ap);
 }
 
-void clear_error() { g_last_error[0] = '\0'; }
+static thread_local uint64_t g_wait_tag    = 0;
+static thread_local int64_t  g_wait_offset = -1;
+static std::atomic<int>      g_force_giveup{0};
+
+void clear_error() {
+    g_last_error[0] = '\0';
+    g_wait_tag      = 0;
+    g_wait_offset   = -1;
+}
+
+void record_wait(uint64_t tag, int64_t status_offset) {
+    g_wait_tag    = tag;
+    g_wait_offset = status_offset;
+}
+
+WaitPlan wait_plan(uint64_t tag, uint32_t default_limit) {
+    if (g_force_giveup.load(std::memory_order_relaxed)) return WaitPlan{~tag, 64u};
+    return WaitPlan{tag, default_limit};
+}
 
 uint64_t next_call_tag() {
     static std::atomic<uint64_t> ctr{0};
@@ -55,4 +73,13 @@ int device_cu_count() {
 
 extern "C" const char *pta_last_error(void) { return pta::g_last_error; }
 
-extern "C" int pta_abi_version(void) { return 5; }
+extern "C" int pta_abi_version(void) { return 6; }
+
+extern "C" int pta_last_wait_status(uint64_t *tag, int64_t *status_offset) {
+    if (tag == nullptr || status_offset == nullptr) return PTA_ERR_INVALID_ARG;
+    *tag           = pta::g_wait_tag;
+    *status_offset = pta::g_wait_offset;
+    return PTA_OK;
+}
+
+extern "C" void pta_test_force_wait_giveup(int on) { pta::g_force_giveup.store(on != 0, std::memory_order_relaxed); }

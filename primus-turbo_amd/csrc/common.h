@@ -59,6 +59,22 @@ uint64_t next_call_tag();
 // call tag would repeat on every replay)
 bool stream_capturing(hipStream_t st);
 
+// Bounded cross-workgroup waits (the single-launch tensorwise quantize, the
+// K split of the GEMM).  A waiting workgroup polls for `expect` at most
+// `spin_limit` times; if it gives up, its result becomes NaN and it writes the
+// call's tag into a status word of the caller's workspace.  wait_plan() gives
+// the values for a call published under `tag` (normally expect == tag; the
+// test hook pta_test_force_wait_giveup makes every wait poll a tag that is
+// never published, with a short limit).  record_wait() notes, per host
+// thread, the tag and the status word's workspace byte offset of the current
+// call; clear_error() resets it to "no bounded wait".
+struct WaitPlan {
+    uint64_t expect;
+    uint32_t spin_limit;
+};
+WaitPlan wait_plan(uint64_t tag, uint32_t default_limit);
+void     record_wait(uint64_t tag, int64_t status_offset);
+
 // compute units of the current device (cached per device)
 int device_cu_count();
 

@@ -56,17 +56,21 @@ int64_t split_tiles(int64_t tiles, int64_t K, int cus) {
 
 constexpr int64_t SPLIT_TILE_BYTES = int64_t(BM) * BN * 4;
 
-// workspace bytes for `n` split tiles (fp32 partial tiles, then one tag each)
-int64_t split_ws_bytes(int64_t n) { return n > 0 ? n * SPLIT_TILE_BYTES + cdiv(n * 8, 256) * 256 : 0; }
+// byte offset of the status word in a K-split workspace for `n` split tiles
+// (after the fp32 partial tiles and one tag each)
+int64_t split_status_offset(int64_t n) { return n * SPLIT_TILE_BYTES + cdiv(n * 8, 256) * 256; }
+
+// workspace bytes for `n` split tiles (partial tiles, tags, status word)
+int64_t split_ws_bytes(int64_t n) { return n > 0 ? split_status_offset(n) + 256 : 0; }
 
 // Entry used by the dense and grouped front ends: NT problem fully described.
 // split_ws: workspace of split_ws_bytes(split_tiles(...)) bytes, or NULL (no
-// K split).
+// K split); split_ws_offset: its byte offset in the caller's workspace.
 int gemm_nt_launch(const uint8_t *a, int fa, int64_t lda, const uint8_t *b, int fb, int64_t ldb,
                    void *c, int out_dt, int64_t ldc, int64_t M, int64_t N, int64_t K, int sm,
                    bool a2d, bool b2d, const void *sa, int64_t sa_m, int64_t sa_k, int64_t sa_bytes,
                    const void *sb, int64_t sb_m, int64_t sb_k, int64_t sb_bytes, hipStream_t st,
-                   uint8_t *split_ws = nullptr) {
+                   uint8_t *split_ws = nullptr, int64_t split_ws_offset = 0) {
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c; g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
     g.sa = sa; g.sb = sb; g.sa_m = sa_m; g.sa_k = sa_k; g.sb_m = sb_m; g.sb_k = sb_k;
@@ -83,10 +87,16 @@ int gemm_nt_launch(const uint8_t *a, int fa, int64_t lda, const uint8_t *b, int 
         // a graph would replay the call tag, so captured calls do not split
         const int64_t ns = split_tiles(int64_t(g.tiles_m) * g.tiles_n, K, device_cu_count());
         if (ns > 0) {
-            g.split_count = static_cast<int>(ns);
-            g.split_ws    = reinterpret_cast<float *>(split_ws);
-            g.split_tags  = reinterpret_cast<uint64_t *>(split_ws + ns * SPLIT_TILE_BYTES);
-            g.split_tag   = next_call_tag();
+            const uint64_t tag = next_call_tag();
+            const WaitPlan w   = wait_plan(tag, SPLIT_SPIN_LIMIT);
+            g.split_count  = static_cast<int>(ns);
+            g.split_ws     = reinterpret_cast<float *>(split_ws);
+            g.split_tags   = reinterpret_cast<uint64_t *>(split_ws + ns * SPLIT_TILE_BYTES);
+            g.split_tag    = tag;
+            g.split_expect = w.expect;
+            g.split_spin   = w.spin_limit;
+            g.split_status = reinterpret_cast<uint64_t *>(split_ws + split_status_offset(ns));
+            record_wait(g.split_tag, split_ws_offset + split_status_offset(ns));
         }
     }
     if (sm == SM_TENSOR) return dispatch_tensor(g, fa, fb, out_dt, st);
@@ -284,7 +294,8 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
         wsp += cdiv(N * K, 256) * 256;
     }
     // what remains of the workspace holds the K split's partial tiles
-    uint8_t *split_ws = split_tiles(cdiv(M, BM) * cdiv(N, BN), K, device_cu_count()) > 0 ? wsp : nullptr;
+    uint8_t      *split_ws  = split_tiles(cdiv(M, BM) * cdiv(N, BN), K, device_cu_count()) > 0 ? wsp : nullptr;
+    const int64_t split_off = workspace != nullptr ? wsp - static_cast<uint8_t *>(workspace) : 0;
     // scale strides in the NT view
     bool    a2d = false, b2d = false;
     int64_t sa_m = 0, sa_k = 0, sb_m = 0, sb_k = 0;
@@ -308,11 +319,12 @@ extern "C" int pta_gemm_fp8(const void *a, int a_fmt, const void *a_scale, int t
     if (sm == SM_MX) { sa_bytes = M * (K / 32); sb_bytes = N * (K / 32); }
     if (!trans_c) {
         return gemm_nt_launch(ap, a_fmt, K, bp, b_fmt, K, c, c_dtype, N, M, N, K, sm, a2d, b2d,
-                              a_scale, sa_m, sa_k, sa_bytes, b_scale, sb_m, sb_k, sb_bytes, st, split_ws);
+                              a_scale, sa_m, sa_k, sa_bytes, b_scale, sb_m, sb_k, sb_bytes, st, split_ws,
+                              split_off);
     }
     // C^T[n, m] = sum_k B'[n,k] A'[m,k]: swap the operands
     return gemm_nt_launch(bp, b_fmt, K, ap, a_fmt, K, c, c_dtype, M, N, M, K, sm, b2d, a2d,
-                          b_scale, sb_m, sb_k, sb_bytes, a_scale, sa_m, sa_k, sa_bytes, st, split_ws);
+                          b_scale, sb_m, sb_k, sb_bytes, a_scale, sa_m, sa_k, sa_bytes, st, split_ws, split_off);
 }
 
 // Whether the kernel-choosing strided entry takes the small-tile kernel: the

@@ -94,9 +94,12 @@ struct GemmArgs {
     // split_ws[q] and then split_tags[q] = split_tag; the second waits for
     // that tag, adds them and stores C.
     int       split_count;
-    float    *split_ws;   // 256 x 256 fp32 per split tile
-    uint64_t *split_tags; // one per split tile
-    uint64_t  split_tag;  // unique per call
+    float    *split_ws;     // 256 x 256 fp32 per split tile
+    uint64_t *split_tags;   // one per split tile
+    uint64_t  split_tag;    // unique per call
+    uint64_t  split_expect; // the tag the second half polls for (split_tag unless a test forces a give-up)
+    unsigned  split_spin;   // polls before the wait gives up
+    uint64_t *split_status; // a wait that gives up writes split_tag here
 };
 
 constexpr unsigned SPLIT_SPIN_LIMIT = 1u << 22; // polls (s_sleep 2 apart) before the wait gives up
@@ -667,17 +670,19 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
                 return;
             }
             // second half: its partner has a lower workgroup id, so it was
-            // dispatched first; the wait is bounded and a timeout gives NaN
+            // dispatched first; the wait is bounded, and a timeout gives NaN
+            // and the call's tag in the status word
             bool seen = true;
             if (t == 0) {
                 unsigned k = 0;
                 while (__hip_atomic_load(&g.split_tags[split_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
-                           g.split_tag &&
-                       k < SPLIT_SPIN_LIMIT) {
+                           g.split_expect &&
+                       k < g.split_spin) {
                     ++k;
                     __builtin_amdgcn_s_sleep(2);
                 }
-                seen = k < SPLIT_SPIN_LIMIT;
+                seen = k < g.split_spin;
+                if (!seen) __hip_atomic_store(g.split_status, g.split_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             const float bad = __syncthreads_or(!seen) ? __builtin_nanf("") : 0.0f;
             // batches of loads small enough for their registers to fit beside

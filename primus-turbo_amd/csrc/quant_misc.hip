@@ -110,22 +110,28 @@ int tw_grid(int64_t n) {
 // tag[i] with device-coherent loads and then reads partial[i] the same way.
 // The tag is unique per call, so a workspace that holds an earlier call's tags
 // needs no clearing, and calls on different streams use their own workspaces.
-// At most TW_FUSED_GRID workgroups of 256 threads and little LDS: they are all
-// resident together on the 256 CUs.  A poll that has not seen every tag after
-// TW_SPIN_LIMIT rounds gives up and the call's scale becomes NaN, so a failure
-// shows in the output instead of hanging.  A tag fixed at graph capture would
-// repeat on every replay, so captured calls use the two-launch form.
+// At most TW_FUSED_GRID workgroups of 256 threads and little LDS (half the
+// CUs of an MI355X at one workgroup each): on an otherwise idle GPU they are
+// all resident together; concurrent work on other streams that holds the CUs
+// for long can keep some of them from starting.  A poll that has not seen
+// every tag after TW_SPIN_LIMIT rounds gives up: the call's scale becomes NaN
+// and the call's tag goes into the status word at TW_STATUS_OFFSET of the
+// workspace (pta_last_wait_status), so a failure shows instead of hanging.  A
+// tag fixed at graph capture would repeat on every replay, so captured calls
+// use the two-launch form.
 constexpr int      TW_FUSED_GRID = 128; // workgroups at most (<= NT: one partial per thread;
                                         // 256 measured slower than the two-launch form)
 constexpr int64_t  TW_FUSED_MAX  = int64_t(TW_FUSED_GRID) * NT * 16 * 4;
 constexpr unsigned TW_SPIN_LIMIT = 1u << 22;
 constexpr size_t   TW_TAG_OFFSET = TW_FUSED_GRID * sizeof(float); // tags after the partials
-static_assert(TW_TAG_OFFSET + TW_FUSED_GRID * sizeof(uint64_t) <= TW_MAX_PARTS * sizeof(float),
-              "partials and tags fit the tensorwise workspace");
+constexpr size_t   TW_STATUS_OFFSET = TW_TAG_OFFSET + TW_FUSED_GRID * sizeof(uint64_t); // then the status word
+static_assert(TW_STATUS_OFFSET + sizeof(uint64_t) <= TW_MAX_PARTS * sizeof(float),
+              "partials, tags and the status word fit the tensorwise workspace");
 
 template <int IN_DT, int FMT, int IT>
 __global__ __launch_bounds__(NT) void tw_fused_kernel(const void *x, int64_t n, uint8_t *q, float *scale_inv,
-                                                      float *partial, uint64_t *tags, uint64_t tag) {
+                                                      float *partial, uint64_t *tags, uint64_t tag,
+                                                      uint64_t expect, unsigned spin_limit, uint64_t *status) {
     const int     tid    = static_cast<int>(threadIdx.x);
     const int     b      = static_cast<int>(blockIdx.x);
     const int     g      = static_cast<int>(gridDim.x);
@@ -167,15 +173,17 @@ __global__ __launch_bounds__(NT) void tw_fused_kernel(const void *x, int64_t n, 
         unsigned k = 0;
         // device-coherent polls; the partial is read (device-coherent) only
         // after its tag has been seen
-        while (__hip_atomic_load(&tags[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag && k < TW_SPIN_LIMIT) {
+        while (__hip_atomic_load(&tags[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != expect &&
+               k < spin_limit) {
             ++k;
             __builtin_amdgcn_s_sleep(2);
         }
         asm volatile("" ::: "memory");
-        seen = k < TW_SPIN_LIMIT;
+        seen = k < spin_limit;
         pa   = __hip_atomic_load(&partial[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const bool all_seen = __syncthreads_and(seen);
+    if (!all_seen && tid == 0) __hip_atomic_store(status, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     pa = max64(pa);
     if ((tid & 63) == 0) s[tid >> 6] = pa; // s[] free again: every read of it precedes __syncthreads_and
     __syncthreads();
@@ -200,11 +208,18 @@ int tw_fused_launch(const void *x, int64_t n, uint8_t *q, float *scale_inv, floa
     const int64_t per  = static_cast<int64_t>(NT) * 16;
     const int     it   = n <= per * TW_FUSED_GRID ? 1 : n <= 2 * per * TW_FUSED_GRID ? 2 : 4;
     const int     g    = static_cast<int>(std::max<int64_t>(1, cdiv(n, per * it)));
-    uint64_t     *tags = reinterpret_cast<uint64_t *>(reinterpret_cast<uint8_t *>(parts) + TW_TAG_OFFSET);
-    const uint64_t tag = next_call_tag();
-    if (it == 1) tw_fused_kernel<IN_DT, FMT, 1><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
-    else if (it == 2) tw_fused_kernel<IN_DT, FMT, 2><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
-    else tw_fused_kernel<IN_DT, FMT, 4><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag);
+    uint8_t       *wsb    = reinterpret_cast<uint8_t *>(parts);
+    uint64_t      *tags   = reinterpret_cast<uint64_t *>(wsb + TW_TAG_OFFSET);
+    uint64_t      *status = reinterpret_cast<uint64_t *>(wsb + TW_STATUS_OFFSET);
+    const uint64_t tag    = next_call_tag();
+    const WaitPlan w      = wait_plan(tag, TW_SPIN_LIMIT);
+    record_wait(tag, static_cast<int64_t>(TW_STATUS_OFFSET));
+#define PTA_TW_GO(IT)                                                                              \
+    tw_fused_kernel<IN_DT, FMT, IT><<<g, NT, 0, st>>>(x, n, q, scale_inv, parts, tags, tag, w.expect, w.spin_limit, status)
+    if (it == 1) PTA_TW_GO(1);
+    else if (it == 2) PTA_TW_GO(2);
+    else PTA_TW_GO(4);
+#undef PTA_TW_GO
     PTA_CHECK_LAUNCH();
     return PTA_OK;
 }

@@ -32,6 +32,8 @@ _vp, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_s
 SIGNATURES = {
     "pta_last_error": (ctypes.c_char_p, []),
     "pta_abi_version": (_i32, []),
+    "pta_last_wait_status": (_i32, [ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int64)]),
+    "pta_test_force_wait_giveup": (None, [_i32]),
     "pta_quantize_fp8_tensorwise_workspace_size": (_sz, [_i64]),
     "pta_quantize_fp8_tensorwise": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
     "pta_quantize_fp8_tensorwise_noalloc": (_i32, [_vp, _i32, _i64, _vp, _vp, _i32, _vp, _vp]),
@@ -147,6 +149,31 @@ def call(name: str, *args) -> None:
     if rc != 0:
         msg = load().pta_last_error().decode("utf-8", "replace")
         raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+# Debug mode (PRIMUS_TURBO_CHECK_WAITS=1): after each call that launched a
+# bounded cross-workgroup wait, synchronize and raise if the wait gave up.
+CHECK_WAITS = os.environ.get("PRIMUS_TURBO_CHECK_WAITS", "0") not in ("", "0")
+
+
+def wait_gave_up(ws) -> bool:
+    """Whether the last call on this thread launched a bounded wait that gave
+    up (synchronizes the current stream).  ``ws`` is the uint8 workspace
+    tensor that call was given."""
+    tag, off = ctypes.c_uint64(0), ctypes.c_int64(-1)
+    load().pta_last_wait_status(ctypes.byref(tag), ctypes.byref(off))
+    if off.value < 0 or ws is None:
+        return False
+    torch.cuda.current_stream(ws.device).synchronize()
+    word = ws[off.value:off.value + 8].cpu().view(torch.int64).item() & 0xFFFFFFFFFFFFFFFF
+    return word == tag.value
+
+
+def check_waits(name: str, ws) -> None:
+    """In debug mode, raise RuntimeError if the last call's bounded wait gave up."""
+    if CHECK_WAITS and wait_gave_up(ws):
+        raise RuntimeError(f"{name}: a cross-workgroup wait gave up (outputs hold NaN); its workgroups "
+                           "could not all run at once (concurrent work holding the CUs?)")
 
 
 def query(name: str, *args) -> int:

@@ -86,6 +86,7 @@ def gemm_fp8_impl(
         _C.ptr(sb), int(trans_b), _C.ptr(out), _C.out_dtype_code(out_dtype), int(trans_c), M, N, K, gran,
         _C.ptr(ws), 0 if ws is None else ws.numel(), _C.stream(a.device),
     )
+    _C.check_waits("gemm_fp8", ws)
     return out
 
 
@@ -138,4 +139,5 @@ def gemm_fp8_nt(
     ws_n = _C.query("pta_gemm_fp8_nt_strided_ws_size", M, N, K, gran, a.stride(0), b.stride(0), sa_bytes, sb_bytes)
     ws = _C.workspace(ws_n, a.device)
     _C.call("pta_gemm_fp8_nt_strided_ws", *args, _C.ptr(ws), 0 if ws is None else ws.numel(), _C.stream(a.device))
+    _C.check_waits("gemm_fp8", ws)
     return out

@@ -50,6 +50,7 @@ def quantize_fp8_tensorwise_impl(
         _C.ptr(q), _C.fp8_code(out_dtype), _C.ptr(scale_inv), _C.ptr(ws), 0 if ws is None else ws.numel(),
         _C.stream(x.device),
     )
+    _C.check_waits("quantize_fp8 (tensorwise)", ws)
     return q, scale_inv
 
 

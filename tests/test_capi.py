@@ -42,7 +42,7 @@ def test_argument_errors_raise_without_gpu():
     from primus_turbo.pytorch import _C
 
     lib = _C.load()
-    assert lib.pta_abi_version() == 5
+    assert lib.pta_abi_version() == 6
     # NULL input: rejected on the host before any HIP call
     rc = lib.pta_quantize_fp8_blockwise(None, 2, 128, 128, 128, 1, None, None, 0, None)
     assert rc == -1
@@ -115,3 +115,16 @@ def test_argument_errors_of_the_grouped_and_moe_entries():
     with pytest.raises(RuntimeError, match="num_local_experts"):
         _C.call("pta_moe_permute_preprocess", p, _C.MOE_MAP_BOOL, 16, 600, 0, 0, 16, 0, p, p, p, p, p, 1 << 20,
                 None)
+
+
+def test_wait_status_without_a_bounded_wait():
+    """pta_last_wait_status reports offset -1 after a call that launched no
+    bounded wait (here: one rejected on the host)."""
+    from primus_turbo.pytorch import _C
+
+    lib = _C.load()
+    lib.pta_quantize_fp8_blockwise(None, 2, 128, 128, 128, 1, None, None, 0, None)
+    tag, off = ctypes.c_uint64(7), ctypes.c_int64(7)
+    assert lib.pta_last_wait_status(ctypes.byref(tag), ctypes.byref(off)) == 0
+    assert off.value == -1
+    assert lib.pta_last_wait_status(None, None) == -1
