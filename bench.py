@@ -81,18 +81,44 @@ def _time_settled(fn, steps: int, settle_ms: float = 40.0):
     return _time_cuda(fn, steps, 0)
 
 
+# the sources of the headline kernel: a traffic figure measured on other
+# sources is stale and is not reported
+_GEMM_SOURCES = ("primus-turbo_amd/csrc/gemm_kernel.h", "primus-turbo_amd/csrc/gemm.hip",
+                 "primus-turbo_amd/csrc/gemm_inst_block.hip", "primus-turbo_amd/csrc/common.h")
+
+
+def gemm_sources_sha256() -> str:
+    """sha256 over the headline kernel's source files (in _GEMM_SOURCES order)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for p in _GEMM_SOURCES:
+        with open(os.path.join(ROOT, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def _traffic_from_profiles(name: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/<name>.txt), if present."""
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/<name>.txt)
+    and where it came from.  The profile records the sha256 of the kernel
+    sources it was measured on; a figure whose sources differ from the current
+    ones is stale and comes back as None."""
     path = os.path.join(ROOT, "profiles", f"{name}.txt")
+    src = {"profile": f"profiles/{name}.txt", "kernel_sources_sha256": None, "current": False}
     if not os.path.exists(path):
-        return None
+        return None, src
+    value = None
     for line in open(path):
-        if line.startswith("hbm_bytes_per_launch:"):
+        key, _, rest = line.partition(":")
+        if key == "hbm_bytes_per_launch":
             try:
-                return float(line.split(":", 1)[1])
+                value = float(rest)
             except ValueError:
-                return None
-    return None
+                value = None
+        elif key == "kernel_sources_sha256":
+            src["kernel_sources_sha256"] = rest.strip()
+    src["current"] = src["kernel_sources_sha256"] == gemm_sources_sha256()
+    return (value if src["current"] else None), src
 
 
 def _settle(fn, settle_ms: float = 40.0) -> float:
@@ -341,7 +367,12 @@ def main():
                     help="end with three 256 MiB device copies (reference for the FETCH/WRITE counters)")
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="only: each BASELINE quantize kernel next to a plain streaming kernel of the same bytes")
+    ap.add_argument("--sources-sha256", action="store_true",
+                    help="only: print the sha256 of the headline kernel's sources (recorded in the traffic profile)")
     args = ap.parse_args()
+    if args.sources_sha256:
+        print(gemm_sources_sha256())
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the FP8 linear path is benchmarked on a "
                                    "single MI355X (multi-GPU sharding is a design note, not a run)",
@@ -422,7 +453,7 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
 
-    traffic = _traffic_from_profiles("gemm_blockwise_nt_4096x18432x7168_traffic")
+    traffic, traffic_src = _traffic_from_profiles("gemm_blockwise_nt_4096x18432x7168_traffic")
     line = {
         "metric": "FP8 GEMM TFLOP/s (% of FP8 MFMA peak); quantize GB/s (% HBM), 1 GPU",
         "value": round(tflops, 2),
@@ -450,6 +481,7 @@ def main():
             "frac": round(tflops / PEAK_FP8_TFLOPS, 4),
             "traffic": traffic,
         },
+        "traffic_source": traffic_src,
         "cpu_baseline": cpu,
         "accuracy": accuracy,
     }
