@@ -317,6 +317,35 @@ def _stream_ceiling(args):
     print(json.dumps({"stream_ceiling": out, "hbm_peak_TBps": 8.0}))
 
 
+def _grouped_steps(args):
+    """Three config-4 grouped layer steps through turbo.ops.grouped_gemm_fp8
+    (segment / weight quantize, persistent forward, dgrad, variable-K wgrad),
+    for counter passes; with --copy-calibration, three 256 MiB copies after."""
+    import torch
+
+    import primus_turbo.pytorch as turbo
+    from primus_turbo.pytorch.core.low_precision import Float8QuantConfig, Format, ScalingGranularity
+
+    g = torch.Generator().manual_seed(1)
+    dev = "cuda:0"
+    lens = _zipf_counts(65536, 32, 28, 0).to(dev)
+    a = torch.randn((65536, 7168), generator=g).bfloat16().to(dev).requires_grad_(True)
+    w = (torch.randn((32, 2048, 7168), generator=g) * 0.02).bfloat16().to(dev).requires_grad_(True)
+    gout = torch.randn((65536, 2048), generator=g).bfloat16().to(dev)
+    cfg = Float8QuantConfig(granularity=ScalingGranularity.BLOCKWISE, format=Format.E4M3, block_size=128)
+    for _ in range(3):
+        a.grad = w.grad = None
+        turbo.ops.grouped_gemm_fp8(a, w, lens, trans_b=True, config=cfg).backward(gout)
+    torch.cuda.synchronize()
+    if args.copy_calibration:
+        x = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+    print(json.dumps({"grouped_steps": 3, "group_lens": [int(v) for v in lens.cpu()]}))
+
+
 def _quant_calls(a, w):
     """Three calls of each BASELINE quantize kernel on its config's shape, for
     the FETCH_SIZE / WRITE_SIZE counter passes (no timing)."""
@@ -360,9 +389,10 @@ def main():
     ap.add_argument("--settle-ms", type=float, default=60.0,
                     help="GPU milliseconds of untimed calls before the warm-up (the clock settles after input setup)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemm", "quant"], default="all",
+    ap.add_argument("--only", choices=["all", "gemm", "quant", "grouped"], default="all",
                     help="gemm: time only the headline GEMM; quant: the headline GEMM, then three calls of each "
-                         "BASELINE quantize kernel (both for counter passes)")
+                         "BASELINE quantize kernel; grouped: three config-4 grouped layer steps (forward, dgrad, "
+                         "variable-K wgrad) and nothing else (all for counter passes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with three 256 MiB device copies (reference for the FETCH/WRITE counters)")
     ap.add_argument("--stream-ceiling", action="store_true",
@@ -380,6 +410,9 @@ def main():
         sys.exit(2)
     if args.stream_ceiling:
         _stream_ceiling(args)
+        return
+    if args.only == "grouped":
+        _grouped_steps(args)
         return
 
     import torch
