@@ -347,9 +347,13 @@ def _grouped_steps(args):
 
 
 def _quant_calls(a, w):
-    """Three calls of each BASELINE quantize kernel on its config's shape, for
-    the FETCH_SIZE / WRITE_SIZE counter passes (no timing)."""
+    """Three calls of each BASELINE quantize kernel on its config's shape, each
+    followed by three calls of the streaming probe moving the same bytes (the
+    pattern --stream-ceiling compares it with), for counter passes (no timing)."""
     import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "primus-turbo_amd", "bench"))
+    import stream_probe
 
     from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
     from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
@@ -375,10 +379,25 @@ def _quant_calls(a, w):
         lambda: quant_fp8_blockwise_segment_m_row_col_impl(x4, e4, 128, lens, offs),
         lambda: quantize_mxfp8_impl(x5, e4, None, 32, with_trans=True, exp_kmajor=True),
     ]
+    stream = torch.cuda.current_stream().cuda_stream
     for f in calls:
+        res = None
         for _ in range(3):
-            f()
+            res = f()
         torch.cuda.synchronize()
+        outs = [t for t in (res if isinstance(res, (tuple, list)) else (res,)) if isinstance(t, torch.Tensor)]
+        wr = sum(t.numel() * t.element_size() for t in outs)
+        del res, outs
+        rd = {0: a, 1: w, 2: x2, 3: x4, 4: x5}[calls.index(f)]
+        rd = rd.numel() * rd.element_size()
+        ratio = 2 if wr < 0.6 * rd else 1
+        wb = (wr if ratio == 2 else (rd + wr) // 2) // 16 * 16
+        src = torch.empty(ratio * wb, dtype=torch.uint8, device=dev)
+        dst = torch.empty(wb, dtype=torch.uint8, device=dev)
+        for _ in range(3):
+            stream_probe.probe(src, dst, wb, ratio, 1, stream)  # non-temporal: the faster form at these sizes
+        torch.cuda.synchronize()
+        del src, dst
 
 
 def main():
