@@ -180,7 +180,7 @@ def query(name: str, *args) -> int:
     """A size query.  Answers are cached per (entry, arguments, current device):
     some sizes depend on the device as well (the GEMM workspaces hold the K
     split's partial tiles, whose use depends on the device's CU count)."""
-    key = (name, args, torch.cuda.current_device() if _gpu_checked else -1)
+    key = (name, args, _cur_device() if _gpu_checked else -1)
     v = _queries.get(key)
     if v is None:
         if len(_queries) >= 4096:  # shapes that vary per call (token counts) must not grow it forever
@@ -198,6 +198,7 @@ def ptr(t) -> int | None:
 
 _gpu_checked = False
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_cur_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 
 
 def stream(device=None) -> int:
