@@ -188,16 +188,49 @@ template <int FMT> __device__ __forceinline__ constexpr float fp8_max() {
     return FMT == PTA_E4M3 ? 448.0f : 57344.0f;
 }
 
-// quant op of the reference: clamp(x * scale, -max, max); fmin/fmax send NaN to +max.
+// quant op of the reference: clamp(x * scale, -max, max) through fminf / fmaxf,
+// which send NaN to +max.  Computed as -med3(x * -scale, -max, max): one
+// v_med3_f32 instead of a min and a max.  x * -scale = -(x * scale) exactly (RNE
+// is sign-symmetric), so for every non-NaN input the result is the reference's
+// clamp, -0 included; a NaN product is always a quiet NaN (an sNaN input is
+// quieted by the multiply), which v_med3_f32 sends to -max (measured on gfx950
+// for both signs), so the negation gives the reference's +max.  The two
+// negations fold into source modifiers of the multiply and of the conversion.
 template <int FMT> __device__ __forceinline__ float qclamp(float x, float scale) {
-    const float v = x * scale;
-    return fmaxf(fminf(v, fp8_max<FMT>()), -fp8_max<FMT>());
+    return -__builtin_amdgcn_fmed3f(x * -scale, -fp8_max<FMT>(), fp8_max<FMT>());
+}
+
+// Four quantized values packed as four fp8 bytes (element 0 in the low byte):
+// each value is -med3(x * -s, -max, max) as in qclamp; the four negations are
+// one xor of the bytes' sign bits after the conversion (fp8 negation flips bit 7,
+// for zeros and the clamped maxima as for every other value).  The first
+// conversion's tied operand is its own first input, whose register is then
+// reused for the result (no zero-initialised register).
+template <int FMT>
+__device__ __forceinline__ uint32_t qpack4s(float x0, float x1, float x2, float x3, float s0, float s1, float s2,
+                                            float s3) {
+    constexpr float M = fp8_max<FMT>();
+    const float     a = __builtin_amdgcn_fmed3f(x0 * -s0, -M, M), b = __builtin_amdgcn_fmed3f(x1 * -s1, -M, M);
+    const float     c = __builtin_amdgcn_fmed3f(x2 * -s2, -M, M), d = __builtin_amdgcn_fmed3f(x3 * -s3, -M, M);
+    int             w;
+    if constexpr (FMT == PTA_E4M3) {
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    } else {
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, __float_as_int(a), false);
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+    }
+    return static_cast<uint32_t>(w) ^ 0x80808080u;
+}
+
+template <int FMT>
+__device__ __forceinline__ uint32_t qpack4(float x0, float x1, float x2, float x3, float scale) {
+    return qpack4s<FMT>(x0, x1, x2, x3, scale, scale, scale, scale);
 }
 
 template <int FMT>
 __device__ __forceinline__ uint32_t quant4(const float *v, float scale) {
-    return cvt4_fp8<FMT>(qclamp<FMT>(v[0], scale), qclamp<FMT>(v[1], scale),
-                         qclamp<FMT>(v[2], scale), qclamp<FMT>(v[3], scale));
+    return qpack4<FMT>(v[0], v[1], v[2], v[3], scale);
 }
 
 // ---- DPP lane exchange (wave64, rows of 16 lanes) ---------------------------

@@ -171,8 +171,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         }
     };
     auto Q4 = [&](int i, int j, float sc) -> uint32_t {
-        return cvt4_fp8<FMT>(qclamp<FMT>(V(i, j), sc), qclamp<FMT>(V(i, j + 1), sc), qclamp<FMT>(V(i, j + 2), sc),
-                             qclamp<FMT>(V(i, j + 3), sc));
+        return qpack4<FMT>(V(i, j), V(i, j + 1), V(i, j + 2), V(i, j + 3), sc);
     };
 
     __shared__ float s_part[16][TILE]; // col partial maxima (16 lane-rows x 128 cols)
@@ -251,8 +250,8 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 uint32_t w[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    w[k] = cvt4_fp8<FMT>(qclamp<FMT>(V(i, 4 * k), cs[4 * k]), qclamp<FMT>(V(i, 4 * k + 1), cs[4 * k + 1]),
-                                         qclamp<FMT>(V(i, 4 * k + 2), cs[4 * k + 2]), qclamp<FMT>(V(i, 4 * k + 3), cs[4 * k + 3]));
+                    w[k] = qpack4s<FMT>(V(i, 4 * k), V(i, 4 * k + 1), V(i, 4 * k + 2), V(i, 4 * k + 3), cs[4 * k],
+                                        cs[4 * k + 1], cs[4 * k + 2], cs[4 * k + 3]);
                 uint8_t *dst = args.q_col + prow * N + n0;
                 if (VEC && n0 + 16 <= N) {
                     st16<(STREAM >= 2)>(dst, w[0], w[1], w[2], w[3]);
@@ -265,13 +264,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         } else {
             // transposed output q_col[N, M]: stage bytes column-major in LDS
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                uint32_t packed = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(V(i, j), cs[j]))) << (8 * i);
-                s_tr[cseg * 16 + j][rgrp] = packed;
-            }
+            for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(V(0, j), V(1, j), V(2, j), V(3, j), cs[j]);
             __syncthreads();
             // 128 output rows (n) x 128 bytes (m): 16-byte chunks; the row stride
             // ldt_col is a multiple of 128 and the padding bytes (rows past M, or
@@ -325,13 +318,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         if constexpr ((MODE & QB_W2D_T) != 0) {
             // transposed copy [B, N, M] through LDS
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                uint32_t packed = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(V(i, j), sc))) << (8 * i);
-                s_tr[cseg * 16 + j][rgrp] = packed;
-            }
+            for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(V(0, j), V(1, j), V(2, j), V(3, j), sc);
             __syncthreads();
             const int64_t ldt = (M + TILE - 1) / TILE * TILE; // padded rows are zero
             uint8_t      *qt  = args.q_t + batch * N * ldt;
