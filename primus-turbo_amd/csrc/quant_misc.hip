@@ -522,11 +522,7 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             }
             const int   e  = mx_e8m0<FMT>(c);
             const float sc = mx_qscale(e);
-            uint32_t    packed = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                packed |= static_cast<uint32_t>(cvt1_fp8<FMT>(qclamp<FMT>(v[i][j], sc))) << (8 * i);
-            s_tr[cseg * 16 + j][rgrp] = packed;
+            s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(v[0][j], v[1][j], v[2][j], v[3][j], sc);
             if ((rgrp & 7) == 0) reinterpret_cast<uint8_t *>(&s_exp[1][cseg * 16 + j])[wave] = static_cast<uint8_t>(e);
         }
         __syncthreads();
