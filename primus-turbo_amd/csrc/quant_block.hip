@@ -67,13 +67,22 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     const int     wave  = t >> 6;
     const int     cseg  = t & 7;
     const int     rgrp  = t >> 3;
+    // Tile order over the flat index (2^31 - 1 tiles at most).  Row-major:
     // consecutive workgroups walk the column tiles of one tile row, so the
-    // workgroups that run together stream whole rows (segment quant 404 ->
-    // 389 us at config 4); the flat index allows 2^31 - 1 tiles
+    // workgroups that run together stream whole input rows.  Column-major:
+    // they walk the tile rows of one column tile, so the transposed copy's
+    // rows are written contiguously.  Measured (one box, alternating):
+    // segment quant 388 us row-major / 404 column-major, 128 x 128 weight
+    // 77.1 / 78.6; weight + transposed copy of 32 experts 376 / 363, headline
+    // activation dual 22.4 / 21.9: the modes that write a transposed copy of
+    // a non-grouped tensor take the column-major order.
+    constexpr bool COLMAJOR = (MODE & QB_SEGMENT) == 0 && (MODE & (QB_COL_T | QB_W2D_T)) != 0;
     const int64_t M = args.M, N = args.N;
     const int64_t tiles_n = (N + TILE - 1) / TILE;
-    const int64_t tm    = static_cast<int64_t>(blockIdx.x) / tiles_n; // tile row (padded space for SEGMENT)
-    const int64_t tn    = static_cast<int64_t>(blockIdx.x) % tiles_n;
+    const int64_t tiles_m = static_cast<int64_t>(gridDim.x) / tiles_n;
+    const int64_t bx      = blockIdx.x;
+    const int64_t tm      = COLMAJOR ? bx % tiles_m : bx / tiles_n; // tile row (padded space for SEGMENT)
+    const int64_t tn      = COLMAJOR ? bx / tiles_m : bx % tiles_n;
     const int64_t batch = blockIdx.z;
     const int64_t n0 = tn * TILE + cseg * 16;
 
