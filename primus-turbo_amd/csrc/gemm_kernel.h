@@ -292,16 +292,19 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
     int            split_half = -1, split_q = 0; // K-split tile: which half, which split tile
     if (g.group_mode == 1) {
         // XCD-aware order: workgroups are dispatched round-robin over the 8
-        // XCDs.  M-tile rows go in blocks of 32: XCD x takes rows 4x .. 4x+3
-        // of each block and walks their N-tiles four rows at a time, so the
-        // tiles one XCD runs together share A rows (8 N-tiles each) and B
-        // tiles (4 rows each, of one group's B) in its L2.  tiles_m is a
+        // XCDs.  M-tile rows go in blocks of 8 R: XCD x takes rows R x ..
+        // R x + R - 1 of each block and walks their N-tiles R rows at a time,
+        // so the tiles one XCD runs together share A rows and B tiles (of one
+        // group's B) in its L2.  R = 4 up to 15 N-tiles, 2 from 16 (measured:
+        // grouped forward at config 4, 8 N-tiles: R = 4 949 us, 2 965, 1 980;
+        // dgrad, 28 N-tiles: R = 2 1019 us, 4 1054, 1 1058).  tiles_m is a
         // multiple of 32 in this mode; surplus rows exit below.
+        const int     rl  = g.tiles_n >= 16 ? 1 : 2; // log2 R
         const int64_t b8  = bid >> 3;
-        const int64_t per = 4 * g.tiles_n; // slots of one XCD's 4-row block
+        const int64_t per = static_cast<int64_t>(g.tiles_n) << rl; // slots of one XCD's R-row block
         const int64_t w   = b8 % per;
-        const int64_t mt  = (b8 / per) * 32 + (bid & 7) * 4 + (w & 3);
-        const int64_t tn  = w >> 2;
+        const int64_t mt  = ((b8 / per) << (rl + 3)) + ((bid & 7) << rl) + (w & ((1 << rl) - 1));
+        const int64_t tn  = w >> rl;
         int64_t       cum = 0, gstart = 0, gend = 0;
         const int64_t grp = find_tile_group(g.group_offs, g.G, mt, cum, gstart, gend);
         if (grp < 0) return; // past the last tile (the tile count is an upper bound)
