@@ -4,10 +4,14 @@
 // One workgroup (4 waves, 256 lanes) owns a 128 x 128 input tile.  Lane t owns
 // 4 consecutive rows (4*(t>>3) .. +3) of a 16-column segment (16*(t&7) .. +15):
 //   * bf16 input is read once with 16-byte loads (a wave covers 8 rows x 256 B);
-//   * row amax = max over the lane's 16 values, then over the 8 consecutive lanes
-//     of the row (3 DPP steps, no LDS);
+//   * row amax = max over the lane's 16 values, then a transposing butterfly
+//     over the 8 lanes of the row group (3 DPP steps, no LDS) that leaves each
+//     lane one row's amax, so each lane divides once; a DPP broadcast hands
+//     every lane its 4 rows' scales;
 //   * col amax = max over the lane's 4 rows, then rotate-by-8 DPP inside each
 //     16-lane row, then a 16 x 128 LDS table reduced by 128 lanes;
+//   * the partial maxima are combined with integer max (exact: they are
+//     non-negative and NaN-free);
 //   * all 64 values stay in VGPRs between the reductions and the casts.
 // Scale arithmetic follows the reference exactly (eps 1e-4, IEEE divides):
 //   primus_turbo/triton/quantization/quant_blockwise.py:11-18 (1-D / dual)
@@ -49,6 +53,18 @@ struct QBArgs {
     int64_t        G;
 };
 
+// Max of two partial maxima of |x|.  They start from +0 and take fmaxf of
+// absolute values, so they are non-negative and never NaN: their bit patterns
+// order as the values do, and the integer max needs none of the NaN-quieting
+// the compiler puts in front of a float max of a DPP-moved operand.
+__device__ __forceinline__ float amax2(float a, float b) {
+    return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+
+// DPP controls beside the ones common to every kernel: broadcast lane 0 / lane
+// 1 of each quad, rotate a 16-lane row by 8
+constexpr int DPP_QUAD_BCAST0 = 0x00, DPP_QUAD_BCAST1 = 0x55, DPP_ROW_ROR8 = 0x128;
+
 // 16-byte output store; non-temporal for streamed (larger than the MALL) inputs,
 // whose outputs do not stay resident either.
 template <bool NT_ST>
@@ -78,11 +94,13 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     // a non-grouped tensor take the column-major order.
     constexpr bool COLMAJOR = (MODE & QB_SEGMENT) == 0 && (MODE & (QB_COL_T | QB_W2D_T)) != 0;
     const int64_t M = args.M, N = args.N;
-    const int64_t tiles_n = (N + TILE - 1) / TILE;
-    const int64_t tiles_m = static_cast<int64_t>(gridDim.x) / tiles_n;
-    const int64_t bx      = blockIdx.x;
-    const int64_t tm      = COLMAJOR ? bx % tiles_m : bx / tiles_n; // tile row (padded space for SEGMENT)
-    const int64_t tn      = COLMAJOR ? bx / tiles_m : bx % tiles_n;
+    // 32-bit index arithmetic: the launch holds at most 2^31 - 1 tiles (a
+    // 64-bit division costs ~150 instructions ahead of the first load)
+    const uint32_t tiles_n = static_cast<uint32_t>((N + TILE - 1) / TILE);
+    const uint32_t tiles_m = gridDim.x / tiles_n;
+    const uint32_t bx      = blockIdx.x;
+    const int64_t  tm      = COLMAJOR ? bx % tiles_m : bx / tiles_n; // tile row (padded space for SEGMENT)
+    const int64_t  tn      = COLMAJOR ? bx / tiles_m : bx % tiles_n;
     const int64_t batch = blockIdx.z;
     const int64_t n0 = tn * TILE + cseg * 16;
 
@@ -120,9 +138,8 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     const char *xb = reinterpret_cast<const char *>(args.x) +
                      batch * args.batch_stride_x * InTraits<IN_DT>::bytes;
 
-    // The lane's 4 x 16 inputs stay packed (8 VGPRs per row for 16-bit types)
-    // and are widened to fp32 at each use: the kernel then fits in few enough
-    // VGPRs that every tile of a large tensor has its loads in flight at once.
+    // The lane's 4 x 16 inputs are loaded packed (8 VGPRs per row for 16-bit
+    // types) and widened to fp32 where used.
     constexpr int CH = InTraits<IN_DT>::bytes; // 16-byte chunks per 16 elements
     uint4 raw[4][CH];
     bool  rvalid[4];
@@ -131,6 +148,10 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         const int64_t r = row_base + rgrp * 4 + i;
         rvalid[i]       = (r >= row_lo) && (r < row_hi);
         if (VEC) {
+            // conditional global loads.  (Loads through a buffer resource that
+            // spans the tile's valid rows, out-of-range rows reading as zero,
+            // issue all eight back to back with no branches, and measured 1-3%
+            // slower on the large streamed tensors, no faster on the rest.)
             typedef unsigned int v4u __attribute__((ext_vector_type(4)));
             const bool   ok = rvalid[i] && n0 + 16 <= N;
             const v4u   *p  = reinterpret_cast<const v4u *>(xb + (r * N + n0) * InTraits<IN_DT>::bytes);
@@ -190,19 +211,42 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
 
     // ---- row direction ----------------------------------------------------
     if constexpr ((MODE & QB_ROW) != 0) {
+        float a[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float a = 0.0f;
+            a[i] = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(V(i, j)));
-            a                = max8(a);
-            const float sc   = scale_from_amax<FMT>(a, 1e-4f);
-            const float sinv = 1.0f / sc;
-            const int64_t r  = row_base + rgrp * 4 + i;
+            for (int j = 0; j < 16; ++j) a[i] = fmaxf(a[i], fabsf(V(i, j)));
+        }
+        // The 8 lanes of a row group hold the same 4 rows.  A transposing
+        // butterfly (partners 7 - c, c ^ 1, c ^ 2; c = cseg) leaves lane c with
+        // the amax of one row, R(c) = 2 (c >= 4) + (c & 1), so each lane divides
+        // once instead of once per row.
+        const bool lo = cseg < 4, odd = (cseg & 1) != 0;
+        float      k0 = lo ? a[0] : a[2], k1 = lo ? a[1] : a[3];
+        k0 = amax2(k0, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(lo ? a[2] : a[0]));
+        k1 = amax2(k1, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(lo ? a[3] : a[1]));
+        float am = odd ? k1 : k0;
+        am       = amax2(am, dpp_f<PTA_DPP_QUAD_XOR1>(odd ? k0 : k1));
+        am       = amax2(am, dpp_f<PTA_DPP_QUAD_XOR2>(am));
+        const float sc_own = scale_from_amax<FMT>(am, 1e-4f);
+        {
+            // lanes 0, 1, 4, 5 of the group store rows 0 .. 3's inverse scales
+            const int64_t r = row_base + rgrp * 4 + (lo ? 0 : 2) + (odd ? 1 : 0);
+            if ((cseg & 2) == 0 && r >= row_lo && r < row_hi) args.s_row[r * args.srow_m + tn * args.srow_k] = 1.0f / sc_own;
+        }
+        // every lane of the group takes the 4 rows' scales: lanes 0 / 1 of each
+        // quad hold rows 0 / 1 (first quad) or 2 / 3 (second quad)
+        const float x = dpp_f<DPP_QUAD_BCAST0>(sc_own), y = dpp_f<DPP_QUAD_BCAST1>(sc_own);
+        const float xm = dpp_f<PTA_DPP_ROW_HALF_MIRROR>(x), ym = dpp_f<PTA_DPP_ROW_HALF_MIRROR>(y);
+        const float sc[4] = {lo ? x : xm, lo ? y : ym, lo ? xm : x, lo ? ym : y};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t r = row_base + rgrp * 4 + i;
             if (rvalid[i]) {
                 uint32_t w[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc);
+                for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc[i]);
                 uint8_t *dst = args.q_row + r * N + n0;
                 if (VEC && n0 + 16 <= N) {
                     st16<(STREAM >= 2)>(dst, w[0], w[1], w[2], w[3]);
@@ -210,9 +254,6 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
 #pragma unroll
                     for (int j = 0; j < 16; ++j)
                         if (n0 + j < N) dst[j] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
-                }
-                if (cseg == 0) {
-                    args.s_row[r * args.srow_m + tn * args.srow_k] = sinv;
                 }
             }
         }
@@ -223,10 +264,10 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         float ca[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            float a = fmaxf(fmaxf(fabsf(V(0, j)), fabsf(V(1, j))), fmaxf(fabsf(V(2, j)), fabsf(V(3, j))));
+            // from +0, so that a column of NaN gives 0 and never NaN (amax2)
+            float a = fmaxf(fmaxf(0.0f, fabsf(V(0, j))), fmaxf(fabsf(V(1, j)), fmaxf(fabsf(V(2, j)), fabsf(V(3, j)))));
             // lanes l and l^8 share a column segment inside each 16-lane row
-            a     = fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x128, 0xf, 0xf, false)));
-            ca[j] = a;
+            ca[j] = amax2(a, dpp_f<DPP_ROW_ROR8>(a));
         }
         if ((lane & 15) < 8) {
             const int prow = wave * 4 + (lane >> 4);
@@ -237,7 +278,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         if (t < TILE) {
             float a = 0.0f;
 #pragma unroll
-            for (int p = 0; p < 16; ++p) a = fmaxf(a, s_part[p][t]);
+            for (int p = 0; p < 16; ++p) a = amax2(a, s_part[p][t]);
             const float sc = scale_from_amax<FMT>(a, 1e-4f);
             s_cscale[t]    = sc;
             const int64_t n = tn * TILE + t;
@@ -325,7 +366,11 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             }
         }
         if constexpr ((MODE & QB_W2D_T) != 0) {
-            // transposed copy [B, N, M] through LDS
+            // transposed copy [B, N, M] through LDS.  The bytes are quantized
+            // again rather than byte-transposed from the row words (8 v_perm per
+            // 16 bytes): the transpose frees 13 VGPRs, the fifth resident
+            // workgroup per CU that buys makes the 940 MB expert stream 2.5%
+            // slower, and at four workgroups both forms take the same time.
 #pragma unroll
             for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(V(0, j), V(1, j), V(2, j), V(3, j), sc);
             __syncthreads();

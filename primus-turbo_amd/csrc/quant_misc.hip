@@ -372,6 +372,22 @@ __global__ __launch_bounds__(NT) void rw_col_quant_kernel(const void *x, int64_t
 // block maximum would saturate (amax * 2^-E > fp8_max).  Both fp8 maxima are
 // 1.75 * 2^emax, so for a normal amax the bump is "mantissa above 1.75"; a
 // subnormal amax clamps to 0 either way.  Biased: e8m0 = clamp(E + 127, 0, 254).
+// Max of two partial maxima of |x| that start from +0 (non-negative, never
+// NaN): their bit patterns order as the values do, so an integer max is exact
+// and needs none of the NaN-quieting the compiler puts in front of a float max
+// of a lane-exchanged operand.
+__device__ __forceinline__ float amax2(float a, float b) {
+    return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+__device__ __forceinline__ float amax_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float amax_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <int FMT> __device__ __forceinline__ int mx_e8m0(float amax) {
     constexpr int  emax = FMT == PTA_E4M3 ? 8 : 15;
     const uint32_t bits = __float_as_uint(amax);
@@ -419,9 +435,9 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     // workgroups that run together stream whole rows (MX dual quantize of
     // 28672 x 8192: 246 -> 205 us; 8192 x 8192: 55.7 -> 54.2 us)
     const int64_t M = a.M, N = a.N;
-    const int64_t tiles_n = a.N_pad / 128;
-    const int64_t tm = static_cast<int64_t>(blockIdx.x) / tiles_n, tn = static_cast<int64_t>(blockIdx.x) % tiles_n,
-                  g  = blockIdx.z;
+    // 32-bit index arithmetic (at most 2^31 - 1 tiles per launch)
+    const uint32_t tiles_n = static_cast<uint32_t>(a.N_pad / 128);
+    const int64_t  tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n, g = blockIdx.z;
     const int64_t n0 = tn * 128 + cseg * 16;
     const char   *xb = reinterpret_cast<const char *>(a.x) + g * M * N * InTraits<IN_DT>::bytes;
 
@@ -480,13 +496,13 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         float m = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[i][j]));
-        m     = fmaxf(m, dpp_f<PTA_DPP_QUAD_XOR1>(m));
+        m     = amax2(m, dpp_f<PTA_DPP_QUAD_XOR1>(m));
         ra[i] = m;
-        blk   = fmaxf(blk, m);
+        blk   = amax2(blk, m);
     }
     if (a.use2d_row || a.use2d_col) {
-        blk = fmaxf(blk, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(blk), 0x128, 0xf, 0xf, false)));
-        blk = max_xor32(max_xor16(blk));
+        blk = amax2(blk, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(blk), 0x128, 0xf, 0xf, false)));
+        blk = amax_xor32(amax_xor16(blk));
     }
 
     // The tile's exponents are staged in LDS and stored as one dword per row
@@ -513,10 +529,11 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         const int64_t       eb_col = a.M_pad / 32;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            float c = fmaxf(fmaxf(fabsf(v[0][j]), fabsf(v[1][j])), fmaxf(fabsf(v[2][j]), fabsf(v[3][j])));
+            // from +0: a column of NaN gives 0, never NaN (amax2)
+            float c = fmaxf(fmaxf(0.0f, fabsf(v[0][j])), fmaxf(fabsf(v[1][j]), fmaxf(fabsf(v[2][j]), fabsf(v[3][j]))));
             if (!a.use2d_col) {
-                c = fmaxf(c, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0x128, 0xf, 0xf, false)));
-                c = max_xor32(max_xor16(c));
+                c = amax2(c, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0x128, 0xf, 0xf, false)));
+                c = amax_xor32(amax_xor16(c));
             } else {
                 c = blk;
             }
