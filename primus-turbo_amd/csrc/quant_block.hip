@@ -61,6 +61,42 @@ __device__ __forceinline__ float amax2(float a, float b) {
     return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
 }
 
+// Cast of four values already scaled into range: no clamp.  Used where no
+// input of the wave (or tile) is NaN or infinite: then |x| <= amax and the
+// scale is max / amax rounded, so |x * scale| <= max (1 + 2^-23) and the
+// round-to-nearest-even cast gives exactly the byte the clamped cast gives.
+template <int FMT>
+__device__ __forceinline__ uint32_t cast4(float a, float b, float c, float d) {
+    uint32_t w;
+    if constexpr (FMT == PTA_E4M3) {
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    } else {
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+    }
+    return w;
+}
+
+// NaN-propagating max of |x| (v_maximum3_f32): the partial maxima it builds
+// are NaN when an input is NaN and equal the NaN-dropping amax otherwise.
+__device__ __forceinline__ float pmax_abs(float a, float x) { return __builtin_elementwise_maximum(a, fabsf(x)); }
+
+// special: the bit pattern of a non-negative partial maximum that is +inf or NaN
+__device__ __forceinline__ bool special_amax(float a) { return __float_as_uint(a) >= 0x7f800000u; }
+
+// wave max of partial maxima (integer max, exact as for amax2)
+__device__ __forceinline__ float amax_wave(float v) {
+    v = amax2(v, dpp_f<PTA_DPP_QUAD_XOR1>(v));
+    v = amax2(v, dpp_f<PTA_DPP_QUAD_XOR2>(v));
+    v = amax2(v, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(v));
+    v = amax2(v, dpp_f<PTA_DPP_ROW_MIRROR>(v));
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v      = amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r      = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // DPP controls beside the ones common to every kernel: broadcast lane 0 / lane
 // 1 of each quad, rotate a 16-lane row by 8
 constexpr int DPP_QUAD_BCAST0 = 0x00, DPP_QUAD_BCAST1 = 0x55, DPP_ROW_ROR8 = 0x128;
@@ -203,32 +239,52 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     auto Q4 = [&](int i, int j, float sc) -> uint32_t {
         return qpack4<FMT>(V(i, j), V(i, j + 1), V(i, j + 2), V(i, j + 3), sc);
     };
+    auto F4 = [&](int i, int j, float sc) -> uint32_t {
+        return cast4<FMT>(V(i, j) * sc, V(i, j + 1) * sc, V(i, j + 2) * sc, V(i, j + 3) * sc);
+    };
+    // NaN or infinity among this wave's inputs: those waves take the
+    // reference's NaN-dropping amax and the clamped cast, the rest the plain
+    // cast (modes without a row pass keep the clamped cast throughout)
+    bool wave_special = (MODE & (QB_ROW | QB_W2D)) == 0;
 
     __shared__ float s_part[16][TILE]; // col partial maxima (16 lane-rows x 128 cols)
     __shared__ float s_cscale[TILE];
-    __shared__ float s_wmax[4];
+    __shared__ float s_wmax[8];
     __shared__ uint32_t s_tr[TILE][TILE / 4 + 1]; // transposed bytes, padded
 
     // ---- row direction ----------------------------------------------------
     if constexpr ((MODE & QB_ROW) != 0) {
-        float a[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            a[i] = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) a[i] = fmaxf(a[i], fabsf(V(i, j)));
-        }
         // The 8 lanes of a row group hold the same 4 rows.  A transposing
         // butterfly (partners 7 - c, c ^ 1, c ^ 2; c = cseg) leaves lane c with
         // the amax of one row, R(c) = 2 (c >= 4) + (c & 1), so each lane divides
         // once instead of once per row.
         const bool lo = cseg < 4, odd = (cseg & 1) != 0;
-        float      k0 = lo ? a[0] : a[2], k1 = lo ? a[1] : a[3];
-        k0 = amax2(k0, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(lo ? a[2] : a[0]));
-        k1 = amax2(k1, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(lo ? a[3] : a[1]));
-        float am = odd ? k1 : k0;
-        am       = amax2(am, dpp_f<PTA_DPP_QUAD_XOR1>(odd ? k0 : k1));
-        am       = amax2(am, dpp_f<PTA_DPP_QUAD_XOR2>(am));
+        auto row_amax = [&](const float (&a)[4]) -> float {
+            float k0 = lo ? a[0] : a[2], k1 = lo ? a[1] : a[3];
+            k0       = amax2(k0, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(lo ? a[2] : a[0]));
+            k1       = amax2(k1, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(lo ? a[3] : a[1]));
+            float am = odd ? k1 : k0;
+            am       = amax2(am, dpp_f<PTA_DPP_QUAD_XOR1>(odd ? k0 : k1));
+            return amax2(am, dpp_f<PTA_DPP_QUAD_XOR2>(am));
+        };
+        float a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a[i] = pmax_abs(a[i], V(i, j));
+        }
+        float am     = row_amax(a);
+        wave_special = __ballot(special_amax(am)) != 0;
+        if (wave_special) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) a[i] = fmaxf(a[i], fabsf(V(i, j)));
+            }
+            am = row_amax(a);
+        }
         const float sc_own = scale_from_amax<FMT>(am, 1e-4f);
         {
             // lanes 0, 1, 4, 5 of the group store rows 0 .. 3's inverse scales
@@ -245,8 +301,13 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             const int64_t r = row_base + rgrp * 4 + i;
             if (rvalid[i]) {
                 uint32_t w[4];
+                if (wave_special) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc[i]);
+                    for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc[i]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) w[k] = F4(i, 4 * k, sc[i]);
+                }
                 uint8_t *dst = args.q_row + r * N + n0;
                 if (VEC && n0 + 16 <= N) {
                     st16<(STREAM >= 2)>(dst, w[0], w[1], w[2], w[3]);
@@ -298,10 +359,17 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 else ok = rvalid[i];
                 if (!ok) continue;
                 uint32_t w[4];
+                if (wave_special) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    w[k] = qpack4s<FMT>(V(i, 4 * k), V(i, 4 * k + 1), V(i, 4 * k + 2), V(i, 4 * k + 3), cs[4 * k],
-                                        cs[4 * k + 1], cs[4 * k + 2], cs[4 * k + 3]);
+                    for (int k = 0; k < 4; ++k)
+                        w[k] = qpack4s<FMT>(V(i, 4 * k), V(i, 4 * k + 1), V(i, 4 * k + 2), V(i, 4 * k + 3), cs[4 * k],
+                                            cs[4 * k + 1], cs[4 * k + 2], cs[4 * k + 3]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        w[k] = cast4<FMT>(V(i, 4 * k) * cs[4 * k], V(i, 4 * k + 1) * cs[4 * k + 1],
+                                          V(i, 4 * k + 2) * cs[4 * k + 2], V(i, 4 * k + 3) * cs[4 * k + 3]);
+                }
                 uint8_t *dst = args.q_col + prow * N + n0;
                 if (VEC && n0 + 16 <= N) {
                     st16<(STREAM >= 2)>(dst, w[0], w[1], w[2], w[3]);
@@ -313,8 +381,14 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             }
         } else {
             // transposed output q_col[N, M]: stage bytes column-major in LDS
+            if (wave_special) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(V(0, j), V(1, j), V(2, j), V(3, j), cs[j]);
+                for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(V(0, j), V(1, j), V(2, j), V(3, j), cs[j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    s_tr[cseg * 16 + j][rgrp] = cast4<FMT>(V(0, j) * cs[j], V(1, j) * cs[j], V(2, j) * cs[j], V(3, j) * cs[j]);
+            }
             __syncthreads();
             // 128 output rows (n) x 128 bytes (m): 16-byte chunks; the row stride
             // ldt_col is a multiple of 128 and the padding bytes (rows past M, or
@@ -336,15 +410,30 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
 
     // ---- 128 x 128 weight tile --------------------------------------------
     if constexpr ((MODE & QB_W2D) != 0) {
+        // one scale for the tile: NaN-propagating amax first; a tile with NaN
+        // or infinity recomputes the reference's NaN-dropping amax and takes
+        // the clamped cast (the decision is the same in all four waves)
         float a = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(V(i, j)));
-        a = max64(a);
+            for (int j = 0; j < 16; ++j) a = pmax_abs(a, V(i, j));
+        a = amax_wave(a);
         if (lane == 0) s_wmax[wave] = a;
         __syncthreads();
-        a = fmaxf(fmaxf(s_wmax[0], s_wmax[1]), fmaxf(s_wmax[2], s_wmax[3]));
+        a            = amax2(amax2(s_wmax[0], s_wmax[1]), amax2(s_wmax[2], s_wmax[3]));
+        wave_special = special_amax(a);
+        if (wave_special) {
+            a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(V(i, j)));
+            a = amax_wave(a);
+            if (lane == 0) s_wmax[4 + wave] = a;
+            __syncthreads();
+            a = amax2(amax2(s_wmax[4], s_wmax[5]), amax2(s_wmax[6], s_wmax[7]));
+        }
         const float   sc  = scale_from_amax<FMT>(a, 1e-4f);
         const int64_t mb  = (M + TILE - 1) / TILE, nb = (N + TILE - 1) / TILE;
         if (t == 0) args.s_w[(batch * mb + tm) * nb + tn] = 1.0f / sc;
@@ -353,8 +442,13 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         for (int i = 0; i < 4; ++i) {
             const int64_t r = row_base + rgrp * 4 + i;
             uint32_t      w[4];
+            if (wave_special) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc);
+                for (int k = 0; k < 4; ++k) w[k] = Q4(i, 4 * k, sc);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) w[k] = F4(i, 4 * k, sc);
+            }
             if (!rvalid[i]) continue;
             uint8_t *dst = qb + r * N + n0;
             if (VEC && n0 + 16 <= N) {
@@ -371,6 +465,8 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             // 16 bytes): the transpose frees 13 VGPRs, the fifth resident
             // workgroup per CU that buys makes the 940 MB expert stream 2.5%
             // slower, and at four workgroups both forms take the same time.
+            // The clamped cast throughout: with the plain cast here the
+            // compiler holds 147 VGPRs (three workgroups per CU).
 #pragma unroll
             for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(V(0, j), V(1, j), V(2, j), V(3, j), sc);
             __syncthreads();
