@@ -53,10 +53,12 @@ struct QBArgs {
     int64_t        G;
 };
 
-// Max of two partial maxima of |x|.  They start from +0 and take fmaxf of
-// absolute values, so they are non-negative and never NaN: their bit patterns
-// order as the values do, and the integer max needs none of the NaN-quieting
-// the compiler puts in front of a float max of a DPP-moved operand.
+// Max of two partial maxima of |x|.  They start from +0, so they are +0 ..
+// +inf, or NaN where the NaN-propagating max built them from a NaN input.
+// Their bit patterns order as the values do and every NaN pattern lies above
+// +inf's, so the integer max is exact and keeps a NaN; it needs none of the
+// NaN-quieting the compiler puts in front of a float max of a lane-exchanged
+// operand.
 __device__ __forceinline__ float amax2(float a, float b) {
     return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
 }

@@ -19,6 +19,55 @@
 namespace pta {
 namespace {
 
+// Max of two partial maxima of |x|.  They start from +0, so they are +0 ..
+// +inf, or NaN where the NaN-propagating max built them from a NaN input.
+// Their bit patterns order as the values do and every NaN pattern lies above
+// +inf's, so the integer max is exact and keeps a NaN; it needs none of the
+// NaN-quieting the compiler puts in front of a float max of a lane-exchanged
+// operand.
+__device__ __forceinline__ float amax2(float a, float b) {
+    return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+__device__ __forceinline__ float amax_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float amax_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// NaN-propagating max of |x| (v_maximum3_f32): NaN when an input is NaN,
+// the NaN-dropping amax otherwise; special: +inf or NaN
+__device__ __forceinline__ float pmax_abs(float a, float x) { return __builtin_elementwise_maximum(a, fabsf(x)); }
+__device__ __forceinline__ bool  special_amax(float a) { return __float_as_uint(a) >= 0x7f800000u; }
+
+// wave max of partial maxima of |x| (integer max, exact as for amax2)
+__device__ __forceinline__ float amax_wave(float v) {
+    v = amax2(v, dpp_f<PTA_DPP_QUAD_XOR1>(v));
+    v = amax2(v, dpp_f<PTA_DPP_QUAD_XOR2>(v));
+    v = amax2(v, dpp_f<PTA_DPP_ROW_HALF_MIRROR>(v));
+    v = amax2(v, dpp_f<PTA_DPP_ROW_MIRROR>(v));
+    return amax_xor32(amax_xor16(v));
+}
+
+// Cast of four values already scaled into range, without the clamp: used
+// where no input is NaN or infinite, so that |x| <= amax and |x * scale| <=
+// max (1 + 2^-23), whose round-to-nearest-even cast is the clamped cast's byte.
+template <int FMT>
+__device__ __forceinline__ uint32_t cast4(float a, float b, float c, float d) {
+    uint32_t w;
+    if constexpr (FMT == PTA_E4M3) {
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    } else {
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+    }
+    return w;
+}
+
+
 constexpr int NT = 256;
 
 // ---------------------------------------------------------------------------
@@ -256,18 +305,36 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
             for (int j = 0; j < 16; ++j) v[c][j] = base + j < len ? load_scalar<IN_DT>(x, off + base + j) : 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[c][j]));
+        for (int j = 0; j < 16; ++j) a = pmax_abs(a, v[c][j]);
     }
+    // a row with NaN or infinity (NaN-propagating amax) recomputes the
+    // reference's NaN-dropping amax and keeps the clamped cast; a given scale
+    // keeps it too.  The decision is uniform over the row's lanes.
     float sc;
+    bool  clamped = true;
     if (scale_in != nullptr) {
         sc = scale_in[row];
     } else {
-        a = max64(a);
-        if constexpr (!WAVE_PER_ROW) {
-            __shared__ float s[NT / 64];
-            if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = a;
-            __syncthreads();
-            a = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        auto row_max = [&](float m) -> float {
+            m = amax_wave(m);
+            if constexpr (!WAVE_PER_ROW) {
+                __shared__ float s[NT / 64];
+                __syncthreads(); // reads of a first pass are done
+                if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = m;
+                __syncthreads();
+                m = amax2(amax2(s[0], s[1]), amax2(s[2], s[3]));
+            }
+            return m;
+        };
+        a       = row_max(a);
+        clamped = special_amax(a);
+        if (clamped) {
+            a = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPT; ++c)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[c][j]));
+            a = row_max(a);
         }
         sc = scale_from_amax<FMT>(a, 1e-12f);
     }
@@ -276,9 +343,18 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
     for (int c = 0; c < CPT; ++c) {
         const int64_t base = (static_cast<int64_t>(c) * LANES + l) * 16;
         if (VEC && base + 16 <= len) {
-            *reinterpret_cast<uint4 *>(q + off + base) =
-                make_uint4(quant4<FMT>(&v[c][0], sc), quant4<FMT>(&v[c][4], sc),
-                           quant4<FMT>(&v[c][8], sc), quant4<FMT>(&v[c][12], sc));
+            uint4 w;
+            if (clamped) {
+                w = make_uint4(quant4<FMT>(&v[c][0], sc), quant4<FMT>(&v[c][4], sc), quant4<FMT>(&v[c][8], sc),
+                               quant4<FMT>(&v[c][12], sc));
+            } else {
+                const float *x = v[c];
+                w = make_uint4(cast4<FMT>(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc),
+                               cast4<FMT>(x[4] * sc, x[5] * sc, x[6] * sc, x[7] * sc),
+                               cast4<FMT>(x[8] * sc, x[9] * sc, x[10] * sc, x[11] * sc),
+                               cast4<FMT>(x[12] * sc, x[13] * sc, x[14] * sc, x[15] * sc));
+            }
+            *reinterpret_cast<uint4 *>(q + off + base) = w;
         } else {
             for (int j = 0; j < 16; ++j)
                 if (base + j < len) q[off + base + j] = cvt1_fp8<FMT>(qclamp<FMT>(v[c][j], sc));
@@ -372,22 +448,6 @@ __global__ __launch_bounds__(NT) void rw_col_quant_kernel(const void *x, int64_t
 // block maximum would saturate (amax * 2^-E > fp8_max).  Both fp8 maxima are
 // 1.75 * 2^emax, so for a normal amax the bump is "mantissa above 1.75"; a
 // subnormal amax clamps to 0 either way.  Biased: e8m0 = clamp(E + 127, 0, 254).
-// Max of two partial maxima of |x| that start from +0 (non-negative, never
-// NaN): their bit patterns order as the values do, so an integer max is exact
-// and needs none of the NaN-quieting the compiler puts in front of a float max
-// of a lane-exchanged operand.
-__device__ __forceinline__ float amax2(float a, float b) {
-    return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
-}
-__device__ __forceinline__ float amax_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float amax_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 template <int FMT> __device__ __forceinline__ int mx_e8m0(float amax) {
     constexpr int  emax = FMT == PTA_E4M3 ? 8 : 15;
     const uint32_t bits = __float_as_uint(amax);
