@@ -587,21 +587,78 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     if constexpr (COL) {
         __shared__ uint32_t s_tr[128][128 / 4 + 1]; // transposed bytes, padded
         const int64_t       eb_col = a.M_pad / 32;
+        // A wave holds one 32-row block; lanes l, l ^ 8, l ^ 16, l ^ 32, ... (the
+        // same cseg) hold its 8 row groups of the same 16 columns.  Column j's
+        // block maximum is reduced by a transposing butterfly that halves the
+        // values per lane at each step: permlane32 and permlane16 swaps (with
+        // two different operands a swap hands the lower half / even rows the
+        // pair's first operand and the others the second, so no selects), then
+        // a row_ror:8 DPP step.  Lane l ends with 2 columns,
+        // jc = 8 (l >= 32) + 4 ((l >> 4) & 1) + 2 ((l >> 3) & 1) + t, computes
+        // their exponents, and the reverse steps broadcast the scales back.
+        const int l    = t & 63;
+        const int jc0  = 8 * (l >> 5) + 4 * ((l >> 4) & 1) + 2 * ((l >> 3) & 1);
+        float     sc16[16];
+        int       e2[2];
+        if (!a.use2d_col) {
+            float ca[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            // from +0: a column of NaN gives 0, never NaN (amax2)
-            float c = fmaxf(fmaxf(0.0f, fabsf(v[0][j])), fmaxf(fabsf(v[1][j]), fmaxf(fabsf(v[2][j]), fabsf(v[3][j]))));
-            if (!a.use2d_col) {
-                c = amax2(c, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0x128, 0xf, 0xf, false)));
-                c = amax_xor32(amax_xor16(c));
-            } else {
-                c = blk;
+            for (int j = 0; j < 16; ++j)
+                // from +0: a column of NaN gives 0, never NaN (amax2)
+                ca[j] = fmaxf(fmaxf(0.0f, fabsf(v[0][j])), fmaxf(fabsf(v[1][j]), fmaxf(fabsf(v[2][j]), fabsf(v[3][j]))));
+            float b8[8], b4[4], b2[2];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(ca[k]), __float_as_uint(ca[k + 8]), false, false);
+                b8[k] = amax2(__uint_as_float(r[0]), __uint_as_float(r[1])); // column 8 (l >= 32) + k
             }
-            const int   e  = mx_e8m0<FMT>(c);
-            const float sc = mx_qscale(e);
-            s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(v[0][j], v[1][j], v[2][j], v[3][j], sc);
-            if ((rgrp & 7) == 0) reinterpret_cast<uint8_t *>(&s_exp[1][cseg * 16 + j])[wave] = static_cast<uint8_t>(e);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(b8[k]), __float_as_uint(b8[k + 4]), false, false);
+                b4[k] = amax2(__uint_as_float(r[0]), __uint_as_float(r[1])); // + 4 ((l >> 4) & 1)
+            }
+            const bool hi8 = (l & 8) != 0;
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                b2[k] = amax2(hi8 ? b4[2 + k] : b4[k],
+                              __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(hi8 ? b4[k] : b4[2 + k]), 0x128, 0xf, 0xf, false)));
+            float s2[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                e2[k] = mx_e8m0<FMT>(b2[k]);
+                s2[k] = mx_qscale(e2[k]);
+            }
+            // reverse: the row_ror:8 partner's pair, then the swaps with equal
+            // operands return (even row's, odd row's) and (lower half's, upper half's)
+            const float p0 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s2[0]), 0x128, 0xf, 0xf, false));
+            const float p1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s2[1]), 0x128, 0xf, 0xf, false));
+            b4[0] = hi8 ? p0 : s2[0];
+            b4[1] = hi8 ? p1 : s2[1];
+            b4[2] = hi8 ? s2[0] : p0;
+            b4[3] = hi8 ? s2[1] : p1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(b4[k]), __float_as_uint(b4[k]), false, false);
+                b8[k]     = __uint_as_float(r[0]);
+                b8[k + 4] = __uint_as_float(r[1]);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(b8[k]), __float_as_uint(b8[k]), false, false);
+                sc16[k]     = __uint_as_float(r[0]);
+                sc16[k + 8] = __uint_as_float(r[1]);
+            }
+        } else {
+            const int   e = mx_e8m0<FMT>(blk);
+            const float s = mx_qscale(e);
+            e2[0] = e2[1] = e;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sc16[j] = s;
         }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) reinterpret_cast<uint8_t *>(&s_exp[1][cseg * 16 + jc0 + k])[wave] = static_cast<uint8_t>(e2[k]);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(v[0][j], v[1][j], v[2][j], v[3][j], sc16[j]);
         __syncthreads();
         if (t < 128 && tn * 128 + t < N) {
             const int64_t n = g * N + tn * 128 + t;
