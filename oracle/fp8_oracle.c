@@ -133,10 +133,10 @@ OR_EXPORT float or_fp8_to_float(uint8_t b, int fmt) {
     return (float)(s ? -v : v);
 }
 
-/* AbsMax op of the reference: fmaxf(fabsf(a), fabsf(b)) -- NaN is dropped.  On
- * the GPU fmaxf quiets a signalling NaN and then returns the other operand, so
- * every NaN is dropped; glibc's fmaxf returns NaN for a signalling NaN (IEEE
- * 754-2008 maxNum), so the NaN test comes first here. */
+/* AbsMax op of the reference: fmaxf(fabsf(a), fabsf(b)) -- every NaN is
+ * dropped, signalling ones included (CUDA's fmaxf returns the other operand for
+ * any NaN).  glibc's fmaxf, like IEEE 754-2008 maxNum, returns NaN for a
+ * signalling NaN, so the NaN test comes first here. */
 static inline float absmax(float acc, float x) { return isnan(x) ? acc : fmaxf(acc, fabsf(x)); }
 
 /* quant op: clamp(x * scale) to [-max, max] (fmin/fmax map NaN to +max), cast. */

@@ -99,6 +99,19 @@ __device__ __forceinline__ float amax_wave(float v) {
     return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// |x| with a signalling NaN first quieted.  v_max / v_max3 of a signalling
+// NaN return NaN, and the next NaN-dropping max then drops that NaN together
+// with the running maximum it replaced; after the quieting every NaN is
+// dropped, as the reference's fmaxf drops it.
+__device__ __forceinline__ float absq(float x) { return fabsf(__builtin_canonicalizef(x)); }
+// the same from an opaque copy of x: each pass forms its quieted values where
+// it uses them, instead of the compiler holding one pass's 64 for the next
+// (+56 VGPRs in the dual kernel, +7 in the MX kernel)
+__device__ __forceinline__ float absq_fresh(float x) {
+    asm volatile("" : "+v"(x));
+    return fabsf(__builtin_canonicalizef(x));
+}
+
 // DPP controls beside the ones common to every kernel: broadcast lane 0 / lane
 // 1 of each quad, rotate a 16-lane row by 8
 constexpr int DPP_QUAD_BCAST0 = 0x00, DPP_QUAD_BCAST1 = 0x55, DPP_ROW_ROR8 = 0x128;
@@ -283,7 +296,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             for (int i = 0; i < 4; ++i) {
                 a[i] = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) a[i] = fmaxf(a[i], fabsf(V(i, j)));
+                for (int j = 0; j < 16; ++j) a[i] = fmaxf(a[i], absq(V(i, j)));
             }
             am = row_amax(a);
         }
@@ -324,14 +337,21 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
 
     // ---- column direction -------------------------------------------------
     if constexpr ((MODE & QB_COL) != 0) {
+        // column maxima from +0, so that a column of NaN gives 0 and never NaN
+        // (amax2); quieted inputs where the wave holds NaN or infinity.  Lanes l
+        // and l ^ 8 share a column segment inside each 16-lane row.
         float ca[16];
+        if (wave_special) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            // from +0, so that a column of NaN gives 0 and never NaN (amax2)
-            float a = fmaxf(fmaxf(0.0f, fabsf(V(0, j))), fmaxf(fabsf(V(1, j)), fmaxf(fabsf(V(2, j)), fabsf(V(3, j)))));
-            // lanes l and l^8 share a column segment inside each 16-lane row
-            ca[j] = amax2(a, dpp_f<DPP_ROW_ROR8>(a));
+            for (int j = 0; j < 16; ++j)
+                ca[j] = fmaxf(fmaxf(0.0f, absq_fresh(V(0, j))), fmaxf(absq_fresh(V(1, j)), fmaxf(absq_fresh(V(2, j)), absq_fresh(V(3, j)))));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                ca[j] = fmaxf(fmaxf(0.0f, fabsf(V(0, j))), fmaxf(fabsf(V(1, j)), fmaxf(fabsf(V(2, j)), fabsf(V(3, j)))));
         }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) ca[j] = amax2(ca[j], dpp_f<DPP_ROW_ROR8>(ca[j]));
         if ((lane & 15) < 8) {
             const int prow = wave * 4 + (lane >> 4);
 #pragma unroll
@@ -430,7 +450,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(V(i, j)));
+                for (int j = 0; j < 16; ++j) a = fmaxf(a, absq(V(i, j)));
             a = amax_wave(a);
             if (lane == 0) s_wmax[4 + wave] = a;
             __syncthreads();

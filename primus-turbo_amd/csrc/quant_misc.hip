@@ -37,6 +37,19 @@ __device__ __forceinline__ float amax_xor32(float v) {
     return amax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// |x| with a signalling NaN first quieted.  v_max / v_max3 of a signalling
+// NaN return NaN, and the next NaN-dropping max then drops that NaN together
+// with the running maximum it replaced; after the quieting every NaN is
+// dropped, as the reference's fmaxf drops it.
+__device__ __forceinline__ float absq(float x) { return fabsf(__builtin_canonicalizef(x)); }
+// the same from an opaque copy of x: each pass forms its quieted values where
+// it uses them, instead of the compiler holding one pass's 64 for the next
+// (+56 VGPRs in the dual kernel, +7 in the MX kernel)
+__device__ __forceinline__ float absq_fresh(float x) {
+    asm volatile("" : "+v"(x));
+    return fabsf(__builtin_canonicalizef(x));
+}
+
 // NaN-propagating max of |x| (v_maximum3_f32): NaN when an input is NaN,
 // the NaN-dropping amax otherwise; special: +inf or NaN
 __device__ __forceinline__ float pmax_abs(float a, float x) { return __builtin_elementwise_maximum(a, fabsf(x)); }
@@ -87,10 +100,10 @@ __global__ __launch_bounds__(NT) void tw_amax_kernel(const void *x, int64_t n, f
             load8<IN_DT>(x, base, v);
             load8<IN_DT>(x, base + 8, w);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a = fmaxf(a, fmaxf(fabsf(v[j]), fabsf(w[j])));
+            for (int j = 0; j < 8; ++j) a = fmaxf(a, fmaxf(absq(v[j]), absq(w[j])));
         } else {
             for (int j = 0; j < 16; ++j)
-                if (base + j < n) a = fmaxf(a, fabsf(load_scalar<IN_DT>(x, base + j)));
+                if (base + j < n) a = fmaxf(a, absq(load_scalar<IN_DT>(x, base + j)));
         }
     }
     a = max64(a);
@@ -202,7 +215,7 @@ __global__ __launch_bounds__(NT) void tw_fused_kernel(const void *x, int64_t n, 
             for (int j = 0; j < 16; ++j) v[it][j] = base + j < n ? load_scalar<IN_DT>(x, base + j) : 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[it][j]));
+        for (int j = 0; j < 16; ++j) a = fmaxf(a, absq(v[it][j]));
     }
     __shared__ float s[NT / 64];
     a = max64(a);
@@ -333,7 +346,7 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
 #pragma unroll
             for (int c = 0; c < CPT; ++c)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[c][j]));
+                for (int j = 0; j < 16; ++j) a = fmaxf(a, absq(v[c][j]));
             a = row_max(a);
         }
         sc = scale_from_amax<FMT>(a, 1e-12f);
@@ -373,7 +386,7 @@ __global__ __launch_bounds__(NT) void rw_last_long_kernel(const void *x, int64_t
         sc = scale_in[row];
     } else {
         float a = 0.0f;
-        for (int64_t i = threadIdx.x; i < len; i += NT) a = fmaxf(a, fabsf(load_scalar<IN_DT>(x, off + i)));
+        for (int64_t i = threadIdx.x; i < len; i += NT) a = fmaxf(a, absq(load_scalar<IN_DT>(x, off + i)));
         a = max64(a);
         __shared__ float s[NT / 64];
         if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = a;
@@ -402,7 +415,7 @@ __global__ __launch_bounds__(NT) void rw_col_partial_kernel(const void *x, int64
     if (n >= inner) return;
     const int64_t r0 = c * RW_CH, r1 = r0 + RW_CH < len ? r0 + RW_CH : len;
     float         a  = 0.0f;
-    for (int64_t r = r0; r < r1; ++r) a = fmaxf(a, fabsf(load_scalar<IN_DT>(x, (o * len + r) * inner + n)));
+    for (int64_t r = r0; r < r1; ++r) a = fmaxf(a, absq(load_scalar<IN_DT>(x, (o * len + r) * inner + n)));
     partial[(o * nchunk + c) * inner + n] = a;
 }
 
@@ -548,18 +561,28 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         }
     }
 
-    // 32 x 32 block maxima (only needed by the 2-D variants)
+    // 1 x 32 row maxima and the lane's share of the 32 x 32 block maxima (the
+    // 2-D variants).  First NaN-propagating: a wave (one 32-row block) with no
+    // NaN or infinity casts without the clamp, since the E8M0 scale brings
+    // every finite value within +-max (|x| 2^(127 - e) <= 1.75 2^emax); a wave
+    // with one recomputes the reference's NaN-dropping maxima and clamps.
     float blk = 0.0f;
     float ra[4];
+    auto  row_maxima = [&](bool propagate) {
+        blk = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float m = 0.0f;
+        for (int i = 0; i < 4; ++i) {
+            float m = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[i][j]));
-        m     = amax2(m, dpp_f<PTA_DPP_QUAD_XOR1>(m));
-        ra[i] = m;
-        blk   = amax2(blk, m);
-    }
+            for (int j = 0; j < 16; ++j) m = propagate ? pmax_abs(m, v[i][j]) : fmaxf(m, absq_fresh(v[i][j]));
+            m     = amax2(m, dpp_f<PTA_DPP_QUAD_XOR1>(m));
+            ra[i] = m;
+            blk   = amax2(blk, m);
+        }
+    };
+    row_maxima(true);
+    const bool wave_special = __ballot(special_amax(blk)) != 0;
+    if (wave_special) row_maxima(false);
     if (a.use2d_row || a.use2d_col) {
         blk = amax2(blk, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(blk), 0x128, 0xf, 0xf, false)));
         blk = amax_xor32(amax_xor16(blk));
@@ -578,8 +601,14 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             const int     e    = mx_e8m0<FMT>(a.use2d_row ? blk : ra[i]);
             const float   sc   = mx_qscale(e);
             uint8_t      *dst  = a.q_row + orow * a.N_pad + n0;
-            *reinterpret_cast<uint4 *>(dst) = make_uint4(quant4<FMT>(&v[i][0], sc), quant4<FMT>(&v[i][4], sc),
-                                                         quant4<FMT>(&v[i][8], sc), quant4<FMT>(&v[i][12], sc));
+            const float  *x    = v[i];
+            *reinterpret_cast<uint4 *>(dst) =
+                wave_special ? make_uint4(quant4<FMT>(&x[0], sc), quant4<FMT>(&x[4], sc), quant4<FMT>(&x[8], sc),
+                                          quant4<FMT>(&x[12], sc))
+                             : make_uint4(cast4<FMT>(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc),
+                                          cast4<FMT>(x[4] * sc, x[5] * sc, x[6] * sc, x[7] * sc),
+                                          cast4<FMT>(x[8] * sc, x[9] * sc, x[10] * sc, x[11] * sc),
+                                          cast4<FMT>(x[12] * sc, x[13] * sc, x[14] * sc, x[15] * sc));
             if ((cseg & 1) == 0) reinterpret_cast<uint8_t *>(&s_exp[0][lr])[cseg >> 1] = static_cast<uint8_t>(e);
         }
     }
@@ -601,11 +630,18 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         float     sc16[16];
         int       e2[2];
         if (!a.use2d_col) {
+            // from +0: a column of NaN gives 0, never NaN (amax2); quieted
+            // inputs where the wave holds NaN or infinity
             float ca[16];
+            if (wave_special) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                // from +0: a column of NaN gives 0, never NaN (amax2)
-                ca[j] = fmaxf(fmaxf(0.0f, fabsf(v[0][j])), fmaxf(fabsf(v[1][j]), fmaxf(fabsf(v[2][j]), fabsf(v[3][j]))));
+                for (int j = 0; j < 16; ++j)
+                    ca[j] = fmaxf(fmaxf(0.0f, absq_fresh(v[0][j])), fmaxf(absq_fresh(v[1][j]), fmaxf(absq_fresh(v[2][j]), absq_fresh(v[3][j]))));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    ca[j] = fmaxf(fmaxf(0.0f, fabsf(v[0][j])), fmaxf(fabsf(v[1][j]), fmaxf(fabsf(v[2][j]), fabsf(v[3][j]))));
+            }
             float b8[8], b4[4], b2[2];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
@@ -657,8 +693,14 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k) reinterpret_cast<uint8_t *>(&s_exp[1][cseg * 16 + jc0 + k])[wave] = static_cast<uint8_t>(e2[k]);
+        if (wave_special) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(v[0][j], v[1][j], v[2][j], v[3][j], sc16[j]);
+            for (int j = 0; j < 16; ++j) s_tr[cseg * 16 + j][rgrp] = qpack4<FMT>(v[0][j], v[1][j], v[2][j], v[3][j], sc16[j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                s_tr[cseg * 16 + j][rgrp] = cast4<FMT>(v[0][j] * sc16[j], v[1][j] * sc16[j], v[2][j] * sc16[j], v[3][j] * sc16[j]);
+        }
         __syncthreads();
         if (t < 128 && tn * 128 + t < N) {
             const int64_t n = g * N + tn * 128 + t;

@@ -123,3 +123,104 @@ def test_blockwise_segment_special(qdt):
     assert_f32_bitexact(f32(sr), o[2], "row scales")
     assert_bytes_equal(u8(qc)[:P], o[1][:P], "padded col bytes")
     assert_f32_bitexact(f32(sc)[: P // 128], o[3][: P // 128], "col scales")
+
+
+@pytest.mark.parametrize("use_2d", [False, True])
+@pytest.mark.parametrize("qdt", FP8)
+def test_mxfp8_special(qdt, use_2d):
+    """MX: exponents and bytes against the oracle's restatement of the rule
+    (NaN-dropping amax, an infinite amax gives exponent 255 - emax, the cast
+    clamped to +-max with NaN to +max), rowwise, colwise and dual."""
+    turbo, SG, SR = _turbo()
+    x = _special_input((256, 512), seed=26)
+    r = SR(use_2d_block=use_2d)
+    for direction, axis in ((1, 1), (0, 0)):
+        q, e = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.MX_BLOCKWISE, block_size=32, axis=axis, scaling_recipe=r)
+        qo, eo = O.quant_mx(x, FMT[qdt], direction, use_2d)
+        assert_bytes_equal(u8(q), qo, f"mx bytes (direction {direction})")
+        assert_bytes_equal(u8(e), eo, f"e8m0 (direction {direction})")
+    qr, er, qc, ec = turbo.ops.quantize_fp8_with_trans(x.cuda(), qdt, SG.MX_BLOCKWISE, block_size=32,
+                                                      scaling_recipe=r, scaling_recipe_for_trans=r)
+    for (qk, ek), direction in (((qr, er), 1), ((qc, ec), 0)):
+        qo, eo = O.quant_mx(x, FMT[qdt], direction, use_2d)
+        assert_bytes_equal(u8(qk), qo, f"dual mx bytes (direction {direction})")
+        assert_bytes_equal(u8(ek), eo, f"dual e8m0 (direction {direction})")
+
+
+def _snan_dense(shape, seed):
+    """N(0,1) bf16 with 6% signalling NaN (both signs) and 4% values x100 at
+    seeded positions: every 16-value lane chunk and every 4-row column run is
+    likely to hold a block maximum ahead of a signalling NaN, where a max that
+    turned the NaN into a running NaN would lose the maximum before it."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=g)
+    big = torch.rand(shape, generator=g) < 0.04
+    x = torch.where(big, x * 100.0, x).to(torch.bfloat16)
+    v = x.view(torch.int16)
+    snan = torch.rand(shape, generator=g) < 0.06
+    neg = torch.rand(shape, generator=g) < 0.5
+    pos_bits = torch.tensor(0x7F81, dtype=torch.int32).to(torch.int16)
+    neg_bits = torch.tensor(0xFF81, dtype=torch.int32).to(torch.int16)
+    v[snan & ~neg] = pos_bits
+    v[snan & neg] = neg_bits
+    return x
+
+
+@pytest.mark.parametrize("qdt", FP8)
+def test_snan_every_quantizer(qdt):
+    """Signalling NaN scattered through the input: amax drops it wherever it
+    falls in a lane's chain (tensorwise, rowwise on both axes, blockwise 1-D,
+    dual, weight, segment and MX in both directions)."""
+    turbo, SG, SR = _turbo()
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_dual_impl, quant_fp8_blockwise_for_weight_impl,
+        quant_fp8_blockwise_segment_m_row_col_impl)
+
+    x = _snan_dense((384, 512), seed=31)
+    q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.TENSORWISE)
+    qo, so = O.quant_tensorwise(x, FMT[qdt])
+    assert_bytes_equal(u8(q), qo, "tensorwise bytes")
+    assert_f32_bitexact(f32(s).reshape(()), so, "tensorwise scale")
+    for axis in (-1, 0):
+        q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.ROWWISE, axis=axis)
+        qo, so = O.quant_rowwise(x, FMT[qdt], axis)
+        assert_bytes_equal(u8(q), qo, f"rowwise bytes (axis {axis})")
+        assert_f32_bitexact(f32(s), so, f"rowwise scales (axis {axis})")
+    for axis in (0, 1):
+        q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.BLOCKWISE, block_size=128, axis=axis)
+        qo, so = O.quant_block1d(x, FMT[qdt], axis)
+        assert_bytes_equal(u8(q), qo, f"blockwise bytes (axis {axis})")
+        assert_f32_bitexact(f32(s), so, f"blockwise scales (axis {axis})")
+    o = O.quant_block_dual(x, FMT[qdt])
+    qr, sr, qc, sc = quant_fp8_blockwise_dual_impl(x.cuda(), qdt, 128)
+    assert_bytes_equal(u8(qr), o[0], "dual row bytes")
+    assert_f32_bitexact(f32(sr), o[1], "dual row scales")
+    assert_bytes_equal(u8(qc), o[2], "dual col bytes")
+    assert_f32_bitexact(f32(sc), o[3], "dual col scales")
+    w = x.reshape(3, 128, 512)
+    q, s, qt = quant_fp8_blockwise_for_weight_impl(w.cuda(), qdt, 128, with_transpose=True)
+    qo, so = O.quant_block_weight(w, FMT[qdt])
+    assert_bytes_equal(u8(q), qo, "weight bytes")
+    assert_f32_bitexact(f32(s), so, "weight scales")
+    assert_bytes_equal(u8(qt), np.ascontiguousarray(np.swapaxes(qo, -1, -2)), "weight transposed bytes")
+    lens = torch.tensor([100, 0, 156, 128], dtype=torch.int64)
+    offs = group_offs_from_lens(lens.cuda())
+    for col_t in (False, True):
+        qr, qc, sr, sc, _, _ = quant_fp8_blockwise_segment_m_row_col_impl(
+            x.cuda(), qdt, 128, lens.cuda(), offs, col_transposed=col_t)
+        o = O.quant_block_segment(x, FMT[qdt], lens.numpy())
+        P = int(o[5][-1])
+        assert_bytes_equal(u8(qr), o[0], "segment row bytes")
+        assert_f32_bitexact(f32(sr), o[2], "segment row scales")
+        qcol = u8(qc)[:, :P].T if col_t else u8(qc)[:P]
+        assert_bytes_equal(np.ascontiguousarray(qcol), o[1][:P], f"segment col bytes (transposed {col_t})")
+        assert_f32_bitexact(f32(sc)[: P // 128], o[3][: P // 128], "segment col scales")
+    for use_2d in (False, True):
+        r = SR(use_2d_block=use_2d)
+        for direction, axis in ((1, 1), (0, 0)):
+            q, e = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.MX_BLOCKWISE, block_size=32, axis=axis,
+                                          scaling_recipe=r)
+            qo, eo = O.quant_mx(x, FMT[qdt], direction, use_2d)
+            assert_bytes_equal(u8(q), qo, f"mx bytes (direction {direction}, 2-D {use_2d})")
+            assert_bytes_equal(u8(e), eo, f"e8m0 (direction {direction}, 2-D {use_2d})")
