@@ -147,27 +147,35 @@ def test_mxfp8_special(qdt, use_2d):
         assert_bytes_equal(u8(ek), eo, f"dual e8m0 (direction {direction})")
 
 
-def _snan_dense(shape, seed):
-    """N(0,1) bf16 with 6% signalling NaN (both signs) and 4% values x100 at
-    seeded positions: every 16-value lane chunk and every 4-row column run is
-    likely to hold a block maximum ahead of a signalling NaN, where a max that
-    turned the NaN into a running NaN would lose the maximum before it."""
+def _snan_dense(shape, seed, dtype=torch.bfloat16):
+    """N(0,1) with 6% signalling NaN (both signs) and 4% values x100 at seeded
+    positions, in bf16, fp16 or fp32: every 16-value lane chunk and every
+    4-row column run is likely to hold a block maximum ahead of a signalling
+    NaN, where a max that turned the NaN into a running NaN would lose the
+    maximum before it."""
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(shape, generator=g)
     big = torch.rand(shape, generator=g) < 0.04
-    x = torch.where(big, x * 100.0, x).to(torch.bfloat16)
-    v = x.view(torch.int16)
+    x = torch.where(big, x * 100.0, x).to(dtype)
     snan = torch.rand(shape, generator=g) < 0.06
     neg = torch.rand(shape, generator=g) < 0.5
-    pos_bits = torch.tensor(0x7F81, dtype=torch.int32).to(torch.int16)
-    neg_bits = torch.tensor(0xFF81, dtype=torch.int32).to(torch.int16)
+    if dtype == torch.float32:
+        v = x.view(torch.int32)
+        pos_bits = torch.tensor(0x7F800001, dtype=torch.int64).to(torch.int32)
+        neg_bits = torch.tensor(0xFF800001, dtype=torch.int64).to(torch.int32)
+    else:  # bf16: 0x7F81; fp16: exponent 11111, quiet bit clear, 0x7D00
+        v = x.view(torch.int16)
+        p, n = (0x7F81, 0xFF81) if dtype == torch.bfloat16 else (0x7D00, 0xFD00)
+        pos_bits = torch.tensor(p, dtype=torch.int32).to(torch.int16)
+        neg_bits = torch.tensor(n, dtype=torch.int32).to(torch.int16)
     v[snan & ~neg] = pos_bits
     v[snan & neg] = neg_bits
     return x
 
 
+@pytest.mark.parametrize("in_dt", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("qdt", FP8)
-def test_snan_every_quantizer(qdt):
+def test_snan_every_quantizer(qdt, in_dt):
     """Signalling NaN scattered through the input: amax drops it wherever it
     falls in a lane's chain (tensorwise, rowwise on both axes, blockwise 1-D,
     dual, weight, segment and MX in both directions)."""
@@ -177,7 +185,7 @@ def test_snan_every_quantizer(qdt):
         quant_fp8_blockwise_dual_impl, quant_fp8_blockwise_for_weight_impl,
         quant_fp8_blockwise_segment_m_row_col_impl)
 
-    x = _snan_dense((384, 512), seed=31)
+    x = _snan_dense((384, 512), seed=31, dtype=in_dt)
     q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.TENSORWISE)
     qo, so = O.quant_tensorwise(x, FMT[qdt])
     assert_bytes_equal(u8(q), qo, "tensorwise bytes")
@@ -216,6 +224,8 @@ def test_snan_every_quantizer(qdt):
         qcol = u8(qc)[:, :P].T if col_t else u8(qc)[:P]
         assert_bytes_equal(np.ascontiguousarray(qcol), o[1][:P], f"segment col bytes (transposed {col_t})")
         assert_f32_bitexact(f32(sc)[: P // 128], o[3][: P // 128], "segment col scales")
+    if in_dt == torch.float32:
+        return  # MX takes bf16 / fp16 inputs only, as the reference asserts
     for use_2d in (False, True):
         r = SR(use_2d_block=use_2d)
         for direction, axis in ((1, 1), (0, 0)):
