@@ -234,3 +234,24 @@ def test_snan_every_quantizer(qdt, in_dt):
             qo, eo = O.quant_mx(x, FMT[qdt], direction, use_2d)
             assert_bytes_equal(u8(q), qo, f"mx bytes (direction {direction}, 2-D {use_2d})")
             assert_bytes_equal(u8(e), eo, f"e8m0 (direction {direction}, 2-D {use_2d})")
+
+
+@pytest.mark.parametrize("qdt", FP8)
+def test_snan_grouped_mx(qdt):
+    """Grouped MX quantize (rows split by group, padded per group) with
+    scattered signalling NaN, against the oracle."""
+    from primus_turbo.pytorch.kernels.grouped_gemm.grouped_gemm_utils import group_offs_from_lens
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import grouped_quantize_mxfp8_impl
+
+    lens = [300, 0, 513, 128, 59]
+    x = _snan_dense((sum(lens), 256), seed=32)
+    gl = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    go = group_offs_from_lens(gl)
+    q_row, e_row, q_col, e_col, _, orw, _, oc = grouped_quantize_mxfp8_impl(x.cuda(), qdt, None, 32, gl, go, True)
+    rq, re, rorw, cq, ce, roc = O.quant_mx_grouped(x, FMT[qdt], lens)
+    assert np.array_equal(orw.cpu().numpy(), rorw) and np.array_equal(oc.cpu().numpy(), roc)
+    R, C = int(rorw[-1]), int(roc[-1])
+    assert_bytes_equal(u8(q_row)[:R], rq[:R], "grouped mx row bytes")
+    assert_bytes_equal(u8(e_row)[:R], re[:R], "grouped mx row exponents")
+    assert_bytes_equal(u8(q_col)[:, :C], cq[:, :C], "grouped mx col bytes")
+    assert_bytes_equal(u8(e_col)[:, : C // 32], ce[:, : C // 32], "grouped mx col exponents")
