@@ -303,7 +303,10 @@ def e8m0_to_scale(e: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
-# dequantization to float64 (exact: fp8 * fp32 fits in fp64)
+# dequantization to float64 (exact: fp8 * fp32 fits in fp64).  The reference
+# multiplies in fp32 and then casts to the output type
+# (csrc/kernels/quantization/quantization_tensorwise.cu:36-42), so a caller
+# rounds these to float32 first and then to the output dtype.
 # ---------------------------------------------------------------------------
 def dequant_tensorwise(q, fmt, s):
     return fp8_to_float(q, fmt).astype(np.float64) * np.float64(np.asarray(s, np.float32))

@@ -106,6 +106,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 }
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    // The value is an fp32 result that then rounds to fp16: the opaque copy keeps the compiler from
+    // fusing the product that made it into v_fma_mix / v_mad_mix, whose single rounding straight to
+    // fp16 differs from fp32-then-fp16 on products that round onto an fp16 midpoint.
+    asm volatile("" : "+v"(f));
     _Float16 h = static_cast<_Float16>(f);
     uint16_t s;
     __builtin_memcpy(&s, &h, 2);

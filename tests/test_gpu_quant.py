@@ -406,23 +406,23 @@ def test_dequant_vs_oracle(qdt, out):
     q, s = turbo.ops.quantize_fp8(xc, qdt, SG.TENSORWISE)
     y = turbo.ops.dequantize_fp8(q, out, SG.TENSORWISE, scale_inv=s)
     ref = O.dequant_tensorwise(u8(q), FMT[qdt], f32(s))
-    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).float().to(out).float().numpy())
     # blockwise 1-D both axes and 2-D
     for axis in (0, 1):
         q, s = turbo.ops.quantize_fp8(xc, qdt, SG.BLOCKWISE, block_size=128, axis=axis)
         y = turbo.ops.dequantize_fp8(q, out, SG.BLOCKWISE, block_size=128, axis=axis, scale_inv=s)
         ref = O.dequant_block1d(u8(q), FMT[qdt], f32(s), axis)
-        np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+        np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).float().to(out).float().numpy())
     r = SR(use_2d_block=True)
     q, s = turbo.ops.quantize_fp8(xc, qdt, SG.BLOCKWISE, block_size=128, scaling_recipe=r)
     y = turbo.ops.dequantize_fp8(q, out, SG.BLOCKWISE, block_size=128, scale_inv=s, scaling_recipe=r)
     ref = O.dequant_block2d(u8(q), FMT[qdt], f32(s))
-    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).float().to(out).float().numpy())
     # rowwise
     q, s = turbo.ops.quantize_fp8(xc, qdt, SG.ROWWISE, axis=-1)
     y = turbo.ops.dequantize_fp8(q, out, SG.ROWWISE, axis=-1, scale_inv=s)
     ref = O.dequant_rowwise(u8(q), FMT[qdt], f32(s))
-    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).to(out).float().numpy())
+    np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).float().to(out).float().numpy())
 
 
 def test_reference_roundtrip_tolerance():

@@ -255,3 +255,41 @@ def test_snan_grouped_mx(qdt):
     assert_bytes_equal(u8(e_row)[:R], re[:R], "grouped mx row exponents")
     assert_bytes_equal(u8(q_col)[:, :C], cq[:, :C], "grouped mx col bytes")
     assert_bytes_equal(u8(e_col)[:, : C // 32], ce[:, : C // 32], "grouped mx col exponents")
+
+
+@pytest.mark.parametrize("out", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("qdt", FP8)
+def test_dequant_every_byte(qdt, out):
+    """Every fp8 byte, the NaN codes (and e5m2's infinities) included, through
+    the tensorwise, rowwise and blockwise (1-D both axes, 2-D) dequantizers,
+    against the oracle's exact decode and float64 product; NaN must come out
+    where the oracle has NaN."""
+    turbo, SG, SR = _turbo()
+    M, N = 256, 512
+    q8 = (torch.arange(M * N, dtype=torch.int64) % 256).to(torch.uint8).view(M, N)
+    q8 = q8[torch.randperm(M, generator=torch.Generator().manual_seed(4))].contiguous()
+    q = q8.view(qdt)
+    g = torch.Generator().manual_seed(5)
+
+    def sc(*shape):
+        return (torch.rand(shape, generator=g) * 3 + 0.01).float()
+
+    def check(y, ref, what):
+        # the reference multiplies in fp32 and then casts (quantization_tensorwise.cu:36-42):
+        # the exact float64 product rounds to fp32 first, then to the output type
+        np.testing.assert_array_equal(f32(y), torch.from_numpy(ref).float().to(out).float().numpy(), err_msg=what)
+
+    s = sc()
+    y = turbo.ops.dequantize_fp8(q.cuda(), out, SG.TENSORWISE, scale_inv=s.cuda())
+    check(y, O.dequant_tensorwise(u8(q), FMT[qdt], s.numpy()), "tensorwise")
+    s = sc(M, 1)
+    y = turbo.ops.dequantize_fp8(q.cuda(), out, SG.ROWWISE, axis=-1, scale_inv=s.cuda())
+    check(y, O.dequant_rowwise(u8(q), FMT[qdt], s.numpy()), "rowwise")
+    for axis, shape in ((1, (M, N // 128)), (0, (M // 128, N))):
+        s = sc(*shape)
+        y = turbo.ops.dequantize_fp8(q.cuda(), out, SG.BLOCKWISE, block_size=128, axis=axis, scale_inv=s.cuda())
+        check(y, O.dequant_block1d(u8(q), FMT[qdt], s.numpy(), axis), f"blockwise axis {axis}")
+    s = sc(M // 128, N // 128)
+    y = turbo.ops.dequantize_fp8(q.cuda(), out, SG.BLOCKWISE, block_size=128, scale_inv=s.cuda(),
+                                 scaling_recipe=SR(use_2d_block=True))
+    check(y, O.dequant_block2d(u8(q), FMT[qdt], s.numpy()), "blockwise 2-D")
