@@ -317,6 +317,122 @@ def _stream_ceiling(args):
     print(json.dumps({"stream_ceiling": out, "hbm_peak_TBps": 8.0}))
 
 
+def _best_ms(fn, n):
+    """Fastest of n calls, each bracketed by its own HIP events on the launch
+    stream, after a 40 ms settle."""
+    import torch
+
+    _settle(fn, 40.0)
+    times = []
+    for _ in range(n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1))
+    return min(times)
+
+
+def _mfma_probe_rates(variants, n):
+    """TFLOP/s of the matrix-pipe probe (primus-turbo_amd/bench/mfma_probe.hip)
+    variants: quantized N(0,1) operand bytes (finite e4m3), four workgroups
+    per CU, ~4 ms per launch, fastest of n launches."""
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "primus-turbo_amd", "bench"))
+    import mfma_probe
+
+    g = torch.Generator().manual_seed(7)
+    ops = torch.randn(mfma_probe.OPERAND_BYTES, generator=g).to(torch.float8_e4m3fn).view(torch.uint8).cuda()
+    wgs, iters = 4 * torch.cuda.get_device_properties(0).multi_processor_count, 500
+    pout = torch.empty(wgs * mfma_probe.THREADS, dtype=torch.float32, device=ops.device)
+    stream = torch.cuda.current_stream().cuda_stream
+    rates = {}
+    for v in variants:
+        ms = _best_ms(lambda v=v: mfma_probe.probe(v, iters, wgs, ops, pout, stream), n)
+        rates[v] = mfma_probe.flops(iters, wgs) / (ms * 1e-3) / 1e12
+    torch.cuda.synchronize()
+    if not bool(torch.isfinite(pout).all()):
+        raise RuntimeError("matrix-pipe probe produced non-finite output")
+    return rates, mfma_probe.VARIANTS
+
+
+def _gemm_ceiling(args):
+    """Each scaled GEMM granularity at the headline shape (4096 x 18432 x
+    7168, NT; the 1x128 x 1x128 case at the config-3 wgrad shape 18432 x 7168
+    x 4096) next to the matrix-pipe probe (primus-turbo_amd/bench/mfma_probe.hip,
+    a library of its own) variant that carries the same per-MFMA work with its
+    operands in registers: no global or LDS traffic.  The probe's rate is the
+    compute ceiling of that granularity's main loop; kernel / probe is what
+    operand delivery, step synchronisation and the epilogue cost on top.
+    Clock settled, one process, best of the timed calls."""
+    import torch
+
+    from primus_turbo.pytorch.core.low_precision import ScalingGranularity
+    from primus_turbo.pytorch.kernels.gemm.gemm_fp8_impl import gemm_fp8_impl, gemm_fp8_nt
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_dual_impl,
+        quant_fp8_blockwise_for_weight_impl,
+        quantize_fp8_tensorwise_impl,
+        quantize_mxfp8_impl,
+    )
+    from primus_turbo.pytorch.ops.gemm_fp8 import _mx_strides
+
+    SG = ScalingGranularity
+    dev = "cuda:0"
+    fdt = torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(0)
+    it = max(10, args.steps // 4)
+
+    probe, names = _mfma_probe_rates([0, 1, 2, 3], it)
+
+    def outl(shape):
+        x = torch.randn(shape, generator=g)
+        idx = torch.randperm(x.numel(), generator=g)[: x.numel() // 1000]
+        x.view(-1)[idx] *= 50.0
+        return x.to(torch.bfloat16).to(dev)
+
+    M, K, N = 4096, 7168, 18432
+    a, w = outl((M, K)), outl((N, K))
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    nbk = K // 128
+    kernels = {}
+    qa, sa = quantize_fp8_tensorwise_impl(a, fdt)
+    qw, sw = quantize_fp8_tensorwise_impl(w, fdt)
+    kernels[0] = (f"tensorwise NT {M}x{N}x{K}", 2.0 * M * N * K,
+                  lambda: gemm_fp8_impl(qa, sa, False, qw, sw, True, torch.bfloat16, False, SG.TENSORWISE.value))
+    a_row, a_s, _, _ = quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True, row_scale_kmajor=True)
+    w_q, w_s = quant_fp8_blockwise_for_weight_impl(w, fdt, 128)
+    kernels[1] = (f"blockwise 1x128 x 128x128 NT {M}x{N}x{K} (headline)", 2.0 * M * N * K,
+                  lambda: gemm_fp8_nt(a_row, w_q, torch.bfloat16, SG.BLOCKWISE, a_s, a_s.stride(), False, w_s,
+                                      (nbk, 1), True, out=out))
+    # wgrad of config 3: dW[N, K] = grad^T a over the M = 4096 tokens, both
+    # operands the quantizer's transposed 1x128 column copies
+    grad = outl((M, N))
+    _, _, g_colT, g_cs = quant_fp8_blockwise_dual_impl(grad, fdt, 128, col_transposed=True)
+    _, _, a_colT, a_cs = quant_fp8_blockwise_dual_impl(a, fdt, 128, col_transposed=True)
+    dw = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    kernels[2] = (f"blockwise 1x128 x 1x128 NT {N}x{K}x{M} (config-3 wgrad)", 2.0 * M * N * K,
+                  lambda: gemm_fp8_nt(g_colT, a_colT, torch.bfloat16, SG.BLOCKWISE, g_cs, (1, N), False, a_cs,
+                                      (1, K), False, out=dw))
+    qa5, ea5 = quantize_mxfp8_impl(a, fdt, 1, 32, exp_kmajor=True)
+    qw5, ew5 = quantize_mxfp8_impl(w, fdt, 1, 32, exp_kmajor=True)
+    kernels[3] = (f"MX NT {M}x{N}x{K}", 2.0 * M * N * K,
+                  lambda: gemm_fp8_nt(qa5, qw5, torch.bfloat16, SG.MX_BLOCKWISE, ea5, _mx_strides(ea5), False, ew5,
+                                      _mx_strides(ew5), False, out=out))
+    res = []
+    for v in sorted(kernels):
+        name, fl, fn = kernels[v]
+        k_tf = fl / (_best_ms(fn, it) * 1e-3) / 1e12
+        res.append({"granularity": names[v], "probe_TFLOPs": round(probe[v], 1),
+                    "probe_frac_of_peak": round(probe[v] / PEAK_FP8_TFLOPS, 3), "kernel": name,
+                    "kernel_TFLOPs": round(k_tf, 1), "kernel_frac_of_peak": round(k_tf / PEAK_FP8_TFLOPS, 3),
+                    "kernel_frac_of_probe": round(k_tf / probe[v], 3)})
+        print(json.dumps({"case_done": name}), file=sys.stderr, flush=True)
+    print(json.dumps({"gemm_ceiling": res, "peak_TFLOPs": PEAK_FP8_TFLOPS}))
+
+
 def _grouped_steps(args):
     """Three config-4 grouped layer steps through turbo.ops.grouped_gemm_fp8
     (segment / weight quantize, persistent forward, dgrad, variable-K wgrad),
@@ -416,6 +532,9 @@ def main():
                     help="end with three 256 MiB device copies (reference for the FETCH/WRITE counters)")
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="only: each BASELINE quantize kernel next to a plain streaming kernel of the same bytes")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="only: each scaled GEMM granularity next to a register-only matrix-pipe kernel carrying "
+                         "the same per-MFMA work")
     ap.add_argument("--sources-sha256", action="store_true",
                     help="only: print the sha256 of the headline kernel's sources (recorded in the traffic profile)")
     args = ap.parse_args()
@@ -429,6 +548,9 @@ def main():
         sys.exit(2)
     if args.stream_ceiling:
         _stream_ceiling(args)
+        return
+    if args.gemm_ceiling:
+        _gemm_ceiling(args)
         return
     if args.only == "grouped":
         _grouped_steps(args)
@@ -477,6 +599,14 @@ def main():
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
     per_call = _per_call_ms(gemm, 100)  # distribution, after (outside) the timed region
+    ceiling = None
+    if args.only == "all":
+        # the compute ceiling of this granularity's main loop: the matrix-pipe
+        # probe with the same MFMAs and scale FMAs, operands in registers
+        rates, names = _mfma_probe_rates([1], 10)
+        ceiling = {"probe": names[1] + ", operands in registers (primus-turbo_amd/bench/mfma_probe.hip)",
+                   "probe_TFLOPs": round(rates[1], 1), "probe_frac_of_peak": round(rates[1] / PEAK_FP8_TFLOPS, 4),
+                   "kernel_frac_of_probe": round(tflops / rates[1], 4)}
 
     extras = {}
     if args.only == "quant":
@@ -534,6 +664,7 @@ def main():
             "traffic": traffic,
         },
         "traffic_source": traffic_src,
+        "compute_ceiling": ceiling,
         "cpu_baseline": cpu,
         "accuracy": accuracy,
     }
