@@ -216,19 +216,35 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
 // row r (blockIdx.y) takes the group with the r-th largest K segment (ties by
 // index), so the longest groups start first and the short ones fill the tail
 // instead of one long group running alone at the end.  Lane q holds group q's
-// length; its rank counts the groups ahead of it, read back with readlane.
-// Up to 64 groups (a rank costs G steps); beyond that the natural order.
-__device__ __forceinline__ int64_t longest_first_group(const int64_t *offs, int64_t G, int64_t r) {
-    if (G > 64) return r;
-    const int lane = threadIdx.x & 63;
-    const int kq   = lane < G ? static_cast<int>(offs[lane + 1] - offs[lane]) : -1;
-    int       rank = 0;
+// bounds and length; its rank counts the groups ahead of it, read back with
+// readlane.  The chosen group's bounds [k0, k1) come from the lane that holds
+// them (no second load before the first operand DMA).  Up to 64 groups (a
+// rank costs G steps); beyond that the natural order.
+__device__ __forceinline__ int64_t longest_first_group(const int64_t *offs, int64_t G, int64_t r, int64_t &k0,
+                                                       int64_t &k1) {
+    if (G > 64) {
+        k0 = offs[r];
+        k1 = offs[r + 1];
+        return r;
+    }
+    const int     lane = threadIdx.x & 63;
+    const int64_t o0   = lane < G ? offs[lane] : 0, o1 = lane < G ? offs[lane + 1] : 0;
+    const int     kq   = lane < G ? static_cast<int>(o1 - o0) : -1;
+    int           rank = 0;
     for (int p = 0; p < static_cast<int>(G); ++p) {
         const int kp = __builtin_amdgcn_readlane(kq, p);
         rank += (kp > kq) || (kp == kq && p < lane);
     }
     const uint64_t hit = __ballot(lane < G && rank == static_cast<int>(r));
-    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__builtin_ctzll(hit)));
+    const int      q   = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__builtin_ctzll(hit)));
+    auto lane64 = [q](int64_t v) {
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), q);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), q);
+        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    k0 = lane64(o0);
+    k1 = lane64(o1);
+    return q;
 }
 
 // Group of M-tile row `mt` in grouped mode 1: the wave computes every group's
@@ -354,9 +370,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const int64_t bid) 
         n0 = static_cast<int64_t>(tile_n) * BN_;
         // the persistent form serves dense and M-grouped problems only
         if (!PERSIST && g.group_mode == 2) {
-            const int64_t q  = longest_first_group(g.group_offs, g.G, blockIdx.y);
-            const int64_t k0 = g.group_offs[q];
-            K       = g.group_offs[q + 1] - k0;
+            int64_t       k0 = 0, k1 = 0;
+            const int64_t q  = longest_first_group(g.group_offs, g.G, blockIdx.y, k0, k1);
+            K       = k1 - k0;
             A       = g.a + k0;
             B       = g.b + k0;
             kb_base = k0 / BK;
