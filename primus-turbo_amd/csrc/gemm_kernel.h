@@ -875,11 +875,15 @@ template <int SM, bool A2D, bool B2D, int FA, int FB, int OUT_DT, int BNT, bool 
 int launch_kernel(const GemmArgs &g, hipStream_t st) {
     auto kern = gemm_nt_kernel<SM, A2D, B2D, FA, FB, OUT_DT, BNT, PERSIST>;
     constexpr size_t smem = TileCfg<BNT>::SMEM;
-    static bool configured = false; // idempotent attribute set, benign race
-    if (!configured) {
+    // the dynamic-LDS attribute is set once per device (a process may drive
+    // several GPUs); idempotent, so a race between threads is benign
+    static bool configured[64] = {};
+    int         dev            = 0;
+    PTA_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64 || !configured[dev]) {
         PTA_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, smem));
-        configured = true;
+        if (dev >= 0 && dev < 64) configured[dev] = true;
     }
     const uint32_t ntiles = static_cast<uint32_t>(g.tiles_m * g.tiles_n);
     const uint32_t np     = static_cast<uint32_t>(g.persistent);
