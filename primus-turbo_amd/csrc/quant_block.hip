@@ -126,7 +126,7 @@ __device__ __forceinline__ void st16(void *dst, uint32_t a, uint32_t b, uint32_t
     else *reinterpret_cast<v4u *>(dst) = v;
 }
 
-// STREAM: 0 plain accesses, 1 non-temporal input loads, 2 also non-temporal output stores.
+// STREAM: 0 plain accesses, 1 non-temporal input loads, 2 non-temporal output stores (plain loads).
 template <int IN_DT, int FMT, int MODE, bool VEC, int STREAM>
 __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     const int     t     = threadIdx.x;
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             for (int c = 0; c < CH; ++c) {
                 v4u w = v4u{0u, 0u, 0u, 0u};
                 if (ok) {
-                    if constexpr (STREAM >= 1) w = __builtin_nontemporal_load(p + c);
+                    if constexpr (STREAM == 1) w = __builtin_nontemporal_load(p + c);
                     else w = p[c];
                 }
                 raw[i][c] = make_uint4(w.x, w.y, w.z, w.w);
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 }
                 uint8_t *dst = args.q_row + r * N + n0;
                 if (VEC && n0 + 16 <= N) {
-                    st16<(STREAM >= 2)>(dst, w[0], w[1], w[2], w[3]);
+                    st16<(STREAM == 2)>(dst, w[0], w[1], w[2], w[3]);
                 } else {
 #pragma unroll
                     for (int j = 0; j < 16; ++j)
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 }
                 uint8_t *dst = args.q_col + prow * N + n0;
                 if (VEC && n0 + 16 <= N) {
-                    st16<(STREAM >= 2)>(dst, w[0], w[1], w[2], w[3]);
+                    st16<(STREAM == 2)>(dst, w[0], w[1], w[2], w[3]);
                 } else {
 #pragma unroll
                     for (int j = 0; j < 16; ++j)
@@ -425,7 +425,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 const int64_t m   = tm * TILE + mc;
                 if (n >= N) continue;
                 const uint32_t *src = &s_tr[nl][mc >> 2];
-                st16<(STREAM >= 2)>(args.q_col + n * ldt + m, src[0], src[1], src[2], src[3]);
+                st16<(STREAM == 2)>(args.q_col + n * ldt + m, src[0], src[1], src[2], src[3]);
             }
         }
     }
@@ -474,7 +474,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
             if (!rvalid[i]) continue;
             uint8_t *dst = qb + r * N + n0;
             if (VEC && n0 + 16 <= N) {
-                st16<(STREAM >= 2)>(dst, w[0], w[1], w[2], w[3]);
+                st16<(STREAM == 2)>(dst, w[0], w[1], w[2], w[3]);
             } else {
 #pragma unroll
                 for (int j = 0; j < 16; ++j)
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
                 const int64_t m  = tm * TILE + mc;
                 if (n >= N) continue;
                 const uint32_t *src = &s_tr[nl][mc >> 2];
-                st16<(STREAM >= 2)>(qt + n * ldt + m, src[0], src[1], src[2], src[3]);
+                st16<(STREAM == 2)>(qt + n * ldt + m, src[0], src[1], src[2], src[3]);
             }
         }
     }
@@ -572,12 +572,14 @@ __global__ __launch_bounds__(256) void offs_to_padded_offs_kernel(const int64_t 
     }
 }
 
-// Inputs larger than this are streamed with non-temporal loads: they cannot
-// stay resident in the 256 MB MALL anyway, and the hint measured 10-12% faster
-// there, while it costs as much on inputs that the MALL still holds.  Outputs
-// larger than the MALL are also stored non-temporally (4-5% faster on the
-// 470-970 MB outputs of the grouped configuration, 3-10% slower on outputs
-// that fit, measured on one box).
+// Inputs larger than this cannot stay resident in the 256 MB MALL.  When the
+// outputs fit in it, the inputs are read with non-temporal loads (1.4% faster
+// on the 264 MB headline weight; the hint costs as much on inputs that the
+// MALL still holds).  When the outputs are larger than the MALL they are
+// stored non-temporally instead, with plain loads: on the 470-1000 MB outputs
+// of the grouped configuration that measured 4-6% faster than non-temporal
+// loads and stores together, and 3% faster than no hint at all (the hints on
+// both streams were 3-10% slower on outputs that fit).
 constexpr int64_t STREAM_BYTES    = 192ll << 20;
 constexpr int64_t NT_STORE_BYTES  = 256ll << 20;
 
