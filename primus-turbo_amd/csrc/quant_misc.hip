@@ -498,7 +498,26 @@ struct MXArgs {
     int64_t        G;
 };
 
-template <int IN_DT, int FMT, bool ROW, bool COL, bool STREAM, bool GROUPED>
+// 16-byte store, optionally non-temporal
+template <bool NT> __device__ __forceinline__ void st_u4(uint8_t *p, uint4 v) {
+    if constexpr (NT) {
+        typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(v4u_t{v.x, v.y, v.z, v.w}, reinterpret_cast<v4u_t *>(p));
+    } else {
+        *reinterpret_cast<uint4 *>(p) = v;
+    }
+}
+
+// MX tile kernel STREAM mode: 0 plain accesses; 1 non-temporal loads (inputs of
+// 192 MiB or more whose fp8 outputs fit the 256 MB MALL); 2 non-temporal
+// stores with plain loads (such inputs with larger outputs; both hints
+// together were slower on the blockwise kernels)
+inline int mx_stream_mode(bool vec, int64_t in_bytes, int64_t out_bytes) {
+    if (!vec || in_bytes < (192ll << 20)) return 0;
+    return out_bytes >= (256ll << 20) ? 2 : 1;
+}
+
+template <int IN_DT, int FMT, bool ROW, bool COL, int STREAM, bool GROUPED>
 __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     const int     t    = threadIdx.x;
     const int     wave = t >> 6;
@@ -547,8 +566,8 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
         if (a.vec) {
             float lo[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             if (ok) {
-                load8<IN_DT, STREAM>(xb, m * N + n0, lo);
-                load8<IN_DT, STREAM>(xb, m * N + n0 + 8, hi);
+                load8<IN_DT, STREAM == 1>(xb, m * N + n0, lo);
+                load8<IN_DT, STREAM == 1>(xb, m * N + n0 + 8, hi);
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -602,13 +621,13 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             const float   sc   = mx_qscale(e);
             uint8_t      *dst  = a.q_row + orow * a.N_pad + n0;
             const float  *x    = v[i];
-            *reinterpret_cast<uint4 *>(dst) =
+            st_u4<STREAM == 2>(dst,
                 wave_special ? make_uint4(quant4<FMT>(&x[0], sc), quant4<FMT>(&x[4], sc), quant4<FMT>(&x[8], sc),
                                           quant4<FMT>(&x[12], sc))
                              : make_uint4(cast4<FMT>(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc),
                                           cast4<FMT>(x[4] * sc, x[5] * sc, x[6] * sc, x[7] * sc),
                                           cast4<FMT>(x[8] * sc, x[9] * sc, x[10] * sc, x[11] * sc),
-                                          cast4<FMT>(x[12] * sc, x[13] * sc, x[14] * sc, x[15] * sc));
+                                          cast4<FMT>(x[12] * sc, x[13] * sc, x[14] * sc, x[15] * sc)));
             if ((cseg & 1) == 0) reinterpret_cast<uint8_t *>(&s_exp[0][lr])[cseg >> 1] = static_cast<uint8_t>(e);
         }
     }
@@ -716,8 +735,7 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
             const int64_t n  = tn * 128 + nl;
             if (n >= N) continue;
             const uint32_t *src = &s_tr[nl][mc >> 2];
-            *reinterpret_cast<uint4 *>(a.q_col + (g * N + n) * a.M_pad + tm * 128 + mc) =
-                make_uint4(src[0], src[1], src[2], src[3]);
+            st_u4<STREAM == 2>(a.q_col + (g * N + n) * a.M_pad + tm * 128 + mc, make_uint4(src[0], src[1], src[2], src[3]));
         }
     }
     if constexpr (ROW) {
@@ -978,11 +996,12 @@ int mx_launch(const void *x, int64_t G, int64_t M, int64_t N, uint8_t *q_row, ui
     a.vec = aligned16(x) ? 1 : 0;
     PTA_CHECK_ARG((a.M_pad / 128) * (a.N_pad / 128) <= 0x7fffffffll, "tensor too large: more than 2^31 - 1 tiles of 128 x 128");
     const dim3 grid(static_cast<uint32_t>((a.M_pad / 128) * (a.N_pad / 128)), 1, static_cast<uint32_t>(G));
-    // inputs beyond the MALL's reach are streamed with non-temporal loads
-    const bool stream = a.vec && G * M * N * InTraits<IN_DT>::bytes >= (192ll << 20);
+    const int  mode = mx_stream_mode(a.vec != 0, G * M * N * InTraits<IN_DT>::bytes,
+                                     G * M * N * ((q_row ? 1 : 0) + (q_col ? 1 : 0)));
 #define PTA_MX_GO(R, C)                                                                            \
-    if (stream) mx_tile_kernel<IN_DT, FMT, R, C, true, false><<<grid, NT, 0, st>>>(a);             \
-    else mx_tile_kernel<IN_DT, FMT, R, C, false, false><<<grid, NT, 0, st>>>(a);
+    if (mode == 2) mx_tile_kernel<IN_DT, FMT, R, C, 2, false><<<grid, NT, 0, st>>>(a);             \
+    else if (mode == 1) mx_tile_kernel<IN_DT, FMT, R, C, 1, false><<<grid, NT, 0, st>>>(a);        \
+    else mx_tile_kernel<IN_DT, FMT, R, C, 0, false><<<grid, NT, 0, st>>>(a);
     if (q_row && q_col) { PTA_MX_GO(true, true) }
     else if (q_row) { PTA_MX_GO(true, false) }
     else { PTA_MX_GO(false, true) }
@@ -1005,10 +1024,12 @@ int mx_grouped_launch(const void *x, int64_t M, int64_t N, int64_t G, const int6
     a.goffs = goffs; a.offs_row = offs_row; a.offs_col = offs_col; a.G = G;
     PTA_CHECK_ARG((a.M_pad / 128) * (a.N_pad / 128) <= 0x7fffffffll, "tensor too large: more than 2^31 - 1 tiles of 128 x 128");
     const dim3 grid(static_cast<uint32_t>((a.M_pad / 128) * (a.N_pad / 128)), 1, 1);
-    const bool stream = a.vec && M * N * InTraits<IN_DT>::bytes >= (192ll << 20);
+    const int  mode = mx_stream_mode(a.vec != 0, M * N * InTraits<IN_DT>::bytes,
+                                     M * N * ((q_row ? 1 : 0) + (q_col ? 1 : 0)));
 #define PTA_MX_GO(R, C)                                                                            \
-    if (stream) mx_tile_kernel<IN_DT, FMT, R, C, true, true><<<grid, NT, 0, st>>>(a);              \
-    else mx_tile_kernel<IN_DT, FMT, R, C, false, true><<<grid, NT, 0, st>>>(a);
+    if (mode == 2) mx_tile_kernel<IN_DT, FMT, R, C, 2, true><<<grid, NT, 0, st>>>(a);              \
+    else if (mode == 1) mx_tile_kernel<IN_DT, FMT, R, C, 1, true><<<grid, NT, 0, st>>>(a);         \
+    else mx_tile_kernel<IN_DT, FMT, R, C, 0, true><<<grid, NT, 0, st>>>(a);
     if (q_row && q_col) { PTA_MX_GO(true, true) }
     else if (q_row) { PTA_MX_GO(true, false) }
     else { PTA_MX_GO(false, true) }
