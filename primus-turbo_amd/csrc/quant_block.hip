@@ -127,9 +127,15 @@ __device__ __forceinline__ void st16(void *dst, uint32_t a, uint32_t b, uint32_t
 }
 
 // STREAM: 0 plain accesses, 1 non-temporal input loads, 2 non-temporal output stores (plain loads).
-template <int IN_DT, int FMT, int MODE, bool VEC, int STREAM>
-__global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
-    const int     t     = threadIdx.x;
+// TPW: tiles per workgroup.  With 2, the workgroup's two halves (256 lanes
+// each) take two neighbouring tiles of one tile row (row-major order) or one
+// tile column (column-major order), so the workgroup reads 512-byte row
+// segments; both halves run the same barriers (the tile-dependent branch of
+// the weight mode is taken by both when either tile needs it).
+template <int IN_DT, int FMT, int MODE, bool VEC, int STREAM, int TPW>
+__global__ __launch_bounds__(NT * TPW) void quant_block_tile_kernel(QBArgs args) {
+    const int     half  = TPW == 2 ? static_cast<int>(threadIdx.x >> 8) : 0;
+    const int     t     = static_cast<int>(threadIdx.x) & (NT - 1);
     const int     lane  = t & 63;
     const int     wave  = t >> 6;
     const int     cseg  = t & 7;
@@ -148,8 +154,8 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     // 32-bit index arithmetic: the launch holds at most 2^31 - 1 tiles (a
     // 64-bit division costs ~150 instructions ahead of the first load)
     const uint32_t tiles_n = static_cast<uint32_t>((N + TILE - 1) / TILE);
-    const uint32_t tiles_m = gridDim.x / tiles_n;
-    const uint32_t bx      = blockIdx.x;
+    const uint32_t tiles_m = gridDim.x * TPW / tiles_n;
+    const uint32_t bx      = blockIdx.x * TPW + half;
     const int64_t  tm      = COLMAJOR ? bx % tiles_m : bx / tiles_n; // tile row (padded space for SEGMENT)
     const int64_t  tn      = COLMAJOR ? bx / tiles_m : bx % tiles_n;
     const int64_t batch = blockIdx.z;
@@ -262,10 +268,14 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
     // cast (modes without a row pass keep the clamped cast throughout)
     bool wave_special = (MODE & (QB_ROW | QB_W2D)) == 0;
 
-    __shared__ float s_part[16][TILE]; // col partial maxima (16 lane-rows x 128 cols)
-    __shared__ float s_cscale[TILE];
-    __shared__ float s_wmax[8];
-    __shared__ uint32_t s_tr[TILE][TILE / 4 + 1]; // transposed bytes, padded
+    __shared__ float    s_part_[TPW][16][TILE]; // col partial maxima (16 lane-rows x 128 cols)
+    __shared__ float    s_cscale_[TPW][TILE];
+    __shared__ float    s_wmax_[TPW][8];
+    __shared__ uint32_t s_tr_[TPW][TILE][TILE / 4 + 1]; // transposed bytes, padded
+    auto &s_part = s_part_[half];
+    auto &s_cscale = s_cscale_[half];
+    auto &s_wmax = s_wmax_[half];
+    auto &s_tr = s_tr_[half];
 
     // ---- row direction ----------------------------------------------------
     if constexpr ((MODE & QB_ROW) != 0) {
@@ -445,6 +455,12 @@ __global__ __launch_bounds__(NT) void quant_block_tile_kernel(QBArgs args) {
         __syncthreads();
         a            = amax2(amax2(s_wmax[0], s_wmax[1]), amax2(s_wmax[2], s_wmax[3]));
         wave_special = special_amax(a);
+        if constexpr (TPW == 2) {
+            // the branch below holds a barrier: both tiles take it when either needs it
+            // (the clamped cast is exact for any tile)
+            const auto &o = s_wmax_[half ^ 1];
+            wave_special  = wave_special || special_amax(amax2(amax2(o[0], o[1]), amax2(o[2], o[3])));
+        }
         if (wave_special) {
             a = 0.0f;
 #pragma unroll
@@ -601,8 +617,22 @@ int launch_tile(const QBArgs &a, int in_dtype, int fmt, dim3 grid, bool vec, hip
     const int64_t nq        = ((MODE & (QB_ROW | QB_W2D)) ? 1 : 0) + ((MODE & QB_COL) ? 1 : 0) + ((MODE & QB_W2D_T) ? 1 : 0);
     const bool    stream    = vec && in_bytes >= STREAM_BYTES;
     const bool    nt_store  = stream && elems * nq >= NT_STORE_BYTES;
+    // two tiles per workgroup for the large (streamed) tensors when the tile
+    // order pairs neighbours within one tile row (row-major) or column
+    constexpr bool COLMAJOR = (MODE & QB_SEGMENT) == 0 && (MODE & (QB_COL_T | QB_W2D_T)) != 0;
+    const uint32_t tiles_n  = static_cast<uint32_t>(cdiv(a.N, static_cast<int64_t>(TILE)));
+    const bool     pair     = stream && (COLMAJOR ? (grid.x / tiles_n) % 2 == 0 : tiles_n % 2 == 0);
+    const dim3     grid2(grid.x / 2, grid.y, grid.z);
 #define PTA_QB_LAUNCH(IDT, F, V, S)                                                                \
-    quant_block_tile_kernel<IDT, F, MODE, V, S><<<grid, NT, 0, st>>>(a)
+    do {                                                                                           \
+        if constexpr (S != 0) {                                                                    \
+            if (pair) {                                                                            \
+                quant_block_tile_kernel<IDT, F, MODE, V, S, 2><<<grid2, 2 * NT, 0, st>>>(a);       \
+                break;                                                                             \
+            }                                                                                      \
+        }                                                                                          \
+        quant_block_tile_kernel<IDT, F, MODE, V, S, 1><<<grid, NT, 0, st>>>(a);                    \
+    } while (0)
 #define PTA_QB_FMT(IDT, V, S)                                                                      \
     if (fmt == PTA_E4M3) PTA_QB_LAUNCH(IDT, PTA_E4M3, V, S);                                       \
     else PTA_QB_LAUNCH(IDT, PTA_E5M2, V, S)
