@@ -517,9 +517,13 @@ inline int mx_stream_mode(bool vec, int64_t in_bytes, int64_t out_bytes) {
     return out_bytes >= (256ll << 20) ? 2 : 1;
 }
 
-template <int IN_DT, int FMT, bool ROW, bool COL, int STREAM, bool GROUPED>
-__global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
-    const int     t    = threadIdx.x;
+// TPW: tiles per workgroup.  With 2 (streamed tensors), the two 256-lane
+// halves take neighbouring tiles of one tile row, so the workgroup reads
+// 512-byte row segments; every barrier below is taken by both halves.
+template <int IN_DT, int FMT, bool ROW, bool COL, int STREAM, bool GROUPED, int TPW>
+__global__ __launch_bounds__(NT * TPW) void mx_tile_kernel(const MXArgs a) {
+    const int     half = TPW == 2 ? static_cast<int>(threadIdx.x >> 8) : 0;
+    const int     t    = static_cast<int>(threadIdx.x) & (NT - 1);
     const int     wave = t >> 6;
     const int     cseg = t & 7;
     const int     rgrp = t >> 3;
@@ -529,7 +533,8 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     const int64_t M = a.M, N = a.N;
     // 32-bit index arithmetic (at most 2^31 - 1 tiles per launch)
     const uint32_t tiles_n = static_cast<uint32_t>(a.N_pad / 128);
-    const int64_t  tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n, g = blockIdx.z;
+    const uint32_t bx = blockIdx.x * TPW + half;
+    const int64_t  tm = bx / tiles_n, tn = bx % tiles_n, g = blockIdx.z;
     const int64_t n0 = tn * 128 + cseg * 16;
     const char   *xb = reinterpret_cast<const char *>(a.x) + g * M * N * InTraits<IN_DT>::bytes;
 
@@ -610,7 +615,8 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     // The tile's exponents are staged in LDS and stored as one dword per row
     // (rowwise: the tile's 4 column blocks; colwise: its 4 row blocks):
     // scattered single-byte stores cost a third of the kernel's time.
-    __shared__ uint32_t s_exp[2][128];
+    __shared__ uint32_t s_exp_[TPW][2][128];
+    auto &s_exp = s_exp_[half];
     if constexpr (ROW) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -633,7 +639,8 @@ __global__ __launch_bounds__(NT) void mx_tile_kernel(const MXArgs a) {
     }
 
     if constexpr (COL) {
-        __shared__ uint32_t s_tr[128][128 / 4 + 1]; // transposed bytes, padded
+        __shared__ uint32_t s_tr_[TPW][128][128 / 4 + 1]; // transposed bytes, padded
+        auto &s_tr = s_tr_[half];
         const int64_t       eb_col = a.M_pad / 32;
         // A wave holds one 32-row block; lanes l, l ^ 8, l ^ 16, l ^ 32, ... (the
         // same cseg) hold its 8 row groups of the same 16 columns.  Column j's
@@ -998,10 +1005,15 @@ int mx_launch(const void *x, int64_t G, int64_t M, int64_t N, uint8_t *q_row, ui
     const dim3 grid(static_cast<uint32_t>((a.M_pad / 128) * (a.N_pad / 128)), 1, static_cast<uint32_t>(G));
     const int  mode = mx_stream_mode(a.vec != 0, G * M * N * InTraits<IN_DT>::bytes,
                                      G * M * N * ((q_row ? 1 : 0) + (q_col ? 1 : 0)));
+    // streamed tensors: two neighbouring tiles of a tile row per workgroup
+    const bool pair = mode != 0 && (a.N_pad / 128) % 2 == 0;
+    const dim3 grid2(grid.x / 2, grid.y, grid.z);
 #define PTA_MX_GO(R, C)                                                                            \
-    if (mode == 2) mx_tile_kernel<IN_DT, FMT, R, C, 2, false><<<grid, NT, 0, st>>>(a);             \
-    else if (mode == 1) mx_tile_kernel<IN_DT, FMT, R, C, 1, false><<<grid, NT, 0, st>>>(a);        \
-    else mx_tile_kernel<IN_DT, FMT, R, C, 0, false><<<grid, NT, 0, st>>>(a);
+    if (mode == 2 && pair) mx_tile_kernel<IN_DT, FMT, R, C, 2, false, 2><<<grid2, 2 * NT, 0, st>>>(a); \
+    else if (mode == 2) mx_tile_kernel<IN_DT, FMT, R, C, 2, false, 1><<<grid, NT, 0, st>>>(a);     \
+    else if (mode == 1 && pair) mx_tile_kernel<IN_DT, FMT, R, C, 1, false, 2><<<grid2, 2 * NT, 0, st>>>(a); \
+    else if (mode == 1) mx_tile_kernel<IN_DT, FMT, R, C, 1, false, 1><<<grid, NT, 0, st>>>(a);     \
+    else mx_tile_kernel<IN_DT, FMT, R, C, 0, false, 1><<<grid, NT, 0, st>>>(a);
     if (q_row && q_col) { PTA_MX_GO(true, true) }
     else if (q_row) { PTA_MX_GO(true, false) }
     else { PTA_MX_GO(false, true) }
@@ -1026,10 +1038,14 @@ int mx_grouped_launch(const void *x, int64_t M, int64_t N, int64_t G, const int6
     const dim3 grid(static_cast<uint32_t>((a.M_pad / 128) * (a.N_pad / 128)), 1, 1);
     const int  mode = mx_stream_mode(a.vec != 0, M * N * InTraits<IN_DT>::bytes,
                                      M * N * ((q_row ? 1 : 0) + (q_col ? 1 : 0)));
+    const bool pair = mode != 0 && (a.N_pad / 128) % 2 == 0;
+    const dim3 grid2(grid.x / 2, grid.y, grid.z);
 #define PTA_MX_GO(R, C)                                                                            \
-    if (mode == 2) mx_tile_kernel<IN_DT, FMT, R, C, 2, true><<<grid, NT, 0, st>>>(a);              \
-    else if (mode == 1) mx_tile_kernel<IN_DT, FMT, R, C, 1, true><<<grid, NT, 0, st>>>(a);         \
-    else mx_tile_kernel<IN_DT, FMT, R, C, 0, true><<<grid, NT, 0, st>>>(a);
+    if (mode == 2 && pair) mx_tile_kernel<IN_DT, FMT, R, C, 2, true, 2><<<grid2, 2 * NT, 0, st>>>(a); \
+    else if (mode == 2) mx_tile_kernel<IN_DT, FMT, R, C, 2, true, 1><<<grid, NT, 0, st>>>(a);      \
+    else if (mode == 1 && pair) mx_tile_kernel<IN_DT, FMT, R, C, 1, true, 2><<<grid2, 2 * NT, 0, st>>>(a); \
+    else if (mode == 1) mx_tile_kernel<IN_DT, FMT, R, C, 1, true, 1><<<grid, NT, 0, st>>>(a);      \
+    else mx_tile_kernel<IN_DT, FMT, R, C, 0, true, 1><<<grid, NT, 0, st>>>(a);
     if (q_row && q_col) { PTA_MX_GO(true, true) }
     else if (q_row) { PTA_MX_GO(true, false) }
     else { PTA_MX_GO(false, true) }
