@@ -293,3 +293,47 @@ def test_dequant_every_byte(qdt, out):
     y = turbo.ops.dequantize_fp8(q.cuda(), out, SG.BLOCKWISE, block_size=128, scale_inv=s.cuda(),
                                  scaling_recipe=SR(use_2d_block=True))
     check(y, O.dequant_block2d(u8(q), FMT[qdt], s.numpy()), "blockwise 2-D")
+
+
+@pytest.mark.parametrize("qdt", FP8)
+def test_streamed_paired_tiles_special(qdt):
+    """Inputs of 192 MiB or more are quantized two neighbouring 128 x 128 tiles
+    per workgroup (neighbours along a tile row, or along a tile column for the
+    modes that write a transposed copy of a non-grouped tensor).  NaN, sNaN and
+    infinities sit in one tile of a pair whose neighbour is clean in either
+    order: the weight mode's recomputation branch (taken by both tiles when
+    either needs it) and the dual kernel's per-wave paths must give the
+    oracle's bytes and scales for both tiles."""
+    from primus_turbo.pytorch.kernels.quantization.quantization_impl import (
+        quant_fp8_blockwise_dual_impl,
+        quant_fp8_blockwise_for_weight_impl,
+    )
+
+    M, N = 8192, 12288  # 192 MiB of bf16: the streamed, paired launch
+    x = randn((M, N), seed=31, outliers=0.001)
+    v = x.view(torch.int16)
+    planted = {(3, 5): 0x7FC0, (100, 7): 0x7F80, (5 * 128 + 1, 11 * 128 + 2): 0x7F81,
+               (M - 1, N - 1): 0xFF80, (40 * 128 + 9, 31 * 128 + 127): 0xFFC0}
+    for (r, c), p in planted.items():
+        v[r, c] = torch.tensor(p, dtype=torch.int32).to(torch.int16)
+    xd = x.cuda()
+    f = FMT[qdt]
+    qo, so = O.quant_block_weight(x, f)
+    q, s, qt = quant_fp8_blockwise_for_weight_impl(xd, qdt, 128, with_transpose=True)
+    assert_bytes_equal(u8(q), qo, "weight bytes (pairs along a tile column)")
+    assert_f32_bitexact(f32(s), so, "weight scales (pairs along a tile column)")
+    assert_bytes_equal(u8(qt), np.ascontiguousarray(qo.T), "weight transposed bytes")
+    del q, s, qt
+    q, s = quant_fp8_blockwise_for_weight_impl(xd, qdt, 128)
+    assert_bytes_equal(u8(q), qo, "weight bytes (pairs along a tile row)")
+    assert_f32_bitexact(f32(s), so, "weight scales (pairs along a tile row)")
+    del q, s, qo, so
+    o = O.quant_block_dual(x, f)
+    qr, sr, qc, sc = quant_fp8_blockwise_dual_impl(xd, qdt, 128)
+    assert_bytes_equal(u8(qr), o[0], "dual row bytes")
+    assert_f32_bitexact(f32(sr), o[1], "dual row scales")
+    assert_bytes_equal(u8(qc), o[2], "dual col bytes")
+    assert_f32_bitexact(f32(sc), o[3], "dual col scales")
+    del qr, sr, qc, sc
+    _, _, qct, _ = quant_fp8_blockwise_dual_impl(xd, qdt, 128, col_transposed=True)
+    assert_bytes_equal(u8(qct), np.ascontiguousarray(o[2].T), "dual transposed col bytes")
