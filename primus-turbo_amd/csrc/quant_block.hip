@@ -126,7 +126,8 @@ __device__ __forceinline__ void st16(void *dst, uint32_t a, uint32_t b, uint32_t
     else *reinterpret_cast<v4u *>(dst) = v;
 }
 
-// STREAM: 0 plain accesses, 1 non-temporal input loads, 2 non-temporal output stores (plain loads).
+// STREAM: 0 plain accesses, 2 non-temporal output stores (loads stay plain: with two tiles per
+// workgroup the non-temporal load hint measured slower).
 // TPW: tiles per workgroup.  With 2, the workgroup's two halves (256 lanes
 // each) take two neighbouring tiles of one tile row (row-major order) or one
 // tile column (column-major order), so the workgroup reads 512-byte row
@@ -215,10 +216,7 @@ __global__ __launch_bounds__(NT * TPW) void quant_block_tile_kernel(QBArgs args)
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 v4u w = v4u{0u, 0u, 0u, 0u};
-                if (ok) {
-                    if constexpr (STREAM == 1) w = __builtin_nontemporal_load(p + c);
-                    else w = p[c];
-                }
+                if (ok) w = p[c];
                 raw[i][c] = make_uint4(w.x, w.y, w.z, w.w);
             }
         } else {
@@ -588,14 +586,14 @@ __global__ __launch_bounds__(256) void offs_to_padded_offs_kernel(const int64_t 
     }
 }
 
-// Inputs larger than this cannot stay resident in the 256 MB MALL.  When the
-// outputs fit in it, the inputs are read with non-temporal loads (1.4% faster
-// on the 264 MB headline weight; the hint costs as much on inputs that the
-// MALL still holds).  When the outputs are larger than the MALL they are
-// stored non-temporally instead, with plain loads: on the 470-1000 MB outputs
-// of the grouped configuration that measured 4-6% faster than non-temporal
-// loads and stores together, and 3% faster than no hint at all (the hints on
-// both streams were 3-10% slower on outputs that fit).
+// Inputs larger than this cannot stay resident in the 256 MB MALL.  They are
+// quantized two tiles per workgroup with plain loads; outputs larger than the
+// MALL are also stored non-temporally.  Measured on the paired kernels: plain
+// loads 2.8% faster than non-temporal ones on the 264 MB headline weight
+// (with one tile per workgroup the load hint had been 1.4% faster); on the
+// 470-1000 MB outputs of the grouped configuration the store hint with plain
+// loads is 4-6% faster than both hints and 3% faster than none (the hints
+// were 3-10% slower on outputs that fit).
 constexpr int64_t STREAM_BYTES    = 192ll << 20;
 constexpr int64_t NT_STORE_BYTES  = 256ll << 20;
 
@@ -625,7 +623,7 @@ int launch_tile(const QBArgs &a, int in_dtype, int fmt, dim3 grid, bool vec, hip
     const dim3     grid2(grid.x / 2, grid.y, grid.z);
 #define PTA_QB_LAUNCH(IDT, F, V, S)                                                                \
     do {                                                                                           \
-        if constexpr (S != 0) {                                                                    \
+        if constexpr (V) {                                                                         \
             if (pair) {                                                                            \
                 quant_block_tile_kernel<IDT, F, MODE, V, S, 2><<<grid2, 2 * NT, 0, st>>>(a);       \
                 break;                                                                             \
@@ -638,7 +636,6 @@ int launch_tile(const QBArgs &a, int in_dtype, int fmt, dim3 grid, bool vec, hip
     else PTA_QB_LAUNCH(IDT, PTA_E5M2, V, S)
 #define PTA_QB_VEC(IDT)                                                                            \
     if (nt_store) { PTA_QB_FMT(IDT, true, 2); }                                                    \
-    else if (stream) { PTA_QB_FMT(IDT, true, 1); }                                                 \
     else if (vec) { PTA_QB_FMT(IDT, true, 0); }                                                    \
     else { PTA_QB_FMT(IDT, false, 0); }
     if (in_dtype == PTA_BF16) { PTA_QB_VEC(PTA_BF16) }
