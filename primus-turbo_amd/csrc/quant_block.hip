@@ -126,8 +126,7 @@ __device__ __forceinline__ void st16(void *dst, uint32_t a, uint32_t b, uint32_t
     else *reinterpret_cast<v4u *>(dst) = v;
 }
 
-// STREAM: 0 plain accesses, 2 non-temporal output stores (loads stay plain: with two tiles per
-// workgroup the non-temporal load hint measured slower).
+// STREAM: 0 plain accesses, 1 non-temporal input loads, 2 non-temporal output stores (plain loads).
 // TPW: tiles per workgroup.  With 2, the workgroup's two halves (256 lanes
 // each) take two neighbouring tiles of one tile row (row-major order) or one
 // tile column (column-major order), so the workgroup reads 512-byte row
@@ -216,7 +215,10 @@ __global__ __launch_bounds__(NT * TPW) void quant_block_tile_kernel(QBArgs args)
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 v4u w = v4u{0u, 0u, 0u, 0u};
-                if (ok) w = p[c];
+                if (ok) {
+                    if constexpr (STREAM == 1) w = __builtin_nontemporal_load(p + c);
+                    else w = p[c];
+                }
                 raw[i][c] = make_uint4(w.x, w.y, w.z, w.w);
             }
         } else {
@@ -587,13 +589,13 @@ __global__ __launch_bounds__(256) void offs_to_padded_offs_kernel(const int64_t 
 }
 
 // Inputs larger than this cannot stay resident in the 256 MB MALL.  They are
-// quantized two tiles per workgroup with plain loads; outputs larger than the
-// MALL are also stored non-temporally.  Measured on the paired kernels: plain
-// loads 2.8% faster than non-temporal ones on the 264 MB headline weight
-// (with one tile per workgroup the load hint had been 1.4% faster); on the
-// 470-1000 MB outputs of the grouped configuration the store hint with plain
-// loads is 4-6% faster than both hints and 3% faster than none (the hints
-// were 3-10% slower on outputs that fit).
+// quantized two tiles per workgroup.  Outputs larger than the MALL are stored
+// non-temporally with plain loads: on the 470-1000 MB outputs of the grouped
+// configuration that is 4-6% faster than both hints and 3% faster than none
+// (the hints were 3-10% slower on outputs that fit).  When the outputs fit,
+// the 128 x 128 weight mode reads with plain loads (2.7% faster than the load
+// hint on the 264 MB headline weight, once tiles were paired) and the 1-D
+// modes with non-temporal loads (1.6-2.2% faster at 28672 x 8192).
 constexpr int64_t STREAM_BYTES    = 192ll << 20;
 constexpr int64_t NT_STORE_BYTES  = 256ll << 20;
 
@@ -615,6 +617,9 @@ int launch_tile(const QBArgs &a, int in_dtype, int fmt, dim3 grid, bool vec, hip
     const int64_t nq        = ((MODE & (QB_ROW | QB_W2D)) ? 1 : 0) + ((MODE & QB_COL) ? 1 : 0) + ((MODE & QB_W2D_T) ? 1 : 0);
     const bool    stream    = vec && in_bytes >= STREAM_BYTES;
     const bool    nt_store  = stream && elems * nq >= NT_STORE_BYTES;
+    // the load hint for the 1-D modes whose outputs fit the MALL (row-only / column-only
+    // 28672 x 8192: 1.6% / 2.2% faster); the 128 x 128 weight mode reads faster without it
+    const bool    nt_load   = stream && !nt_store && (MODE & QB_W2D) == 0;
     // two tiles per workgroup for the large (streamed) tensors when the tile
     // order pairs neighbours within one tile row (row-major) or column
     constexpr bool COLMAJOR = (MODE & QB_SEGMENT) == 0 && (MODE & (QB_COL_T | QB_W2D_T)) != 0;
@@ -636,6 +641,7 @@ int launch_tile(const QBArgs &a, int in_dtype, int fmt, dim3 grid, bool vec, hip
     else PTA_QB_LAUNCH(IDT, PTA_E5M2, V, S)
 #define PTA_QB_VEC(IDT)                                                                            \
     if (nt_store) { PTA_QB_FMT(IDT, true, 2); }                                                    \
+    else if (nt_load) { PTA_QB_FMT(IDT, true, 1); }                                                \
     else if (vec) { PTA_QB_FMT(IDT, true, 0); }                                                    \
     else { PTA_QB_FMT(IDT, false, 0); }
     if (in_dtype == PTA_BF16) { PTA_QB_VEC(PTA_BF16) }
