@@ -302,12 +302,59 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
     if (WAVE_PER_ROW && row >= rows) return; // whole wave exits together
     const int64_t off = row * len;
 
-    float v[CPT][16];
+    // 16-bit inputs of a vector wave-per-row launch stay packed (8 VGPRs per 16
+    // values instead of 16) and are widened again in each pass that uses
+    // them: the kernel then fits 8 waves per SIMD
+    constexpr bool PACK = VEC && WAVE_PER_ROW && IN_DT != PTA_F32;
+    float    v[PACK ? 1 : CPT][16];
+    uint32_t raw[PACK ? CPT : 1][8];
+    auto get16 = [&](int c, float (&o)[16]) {
+        if constexpr (PACK) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if constexpr (IN_DT == PTA_BF16) {
+                    o[2 * i]     = __uint_as_float(raw[c][i] << 16);
+                    o[2 * i + 1] = __uint_as_float(raw[c][i] & 0xffff0000u);
+                } else {
+                    o[2 * i]     = f16_bits_to_f32(raw[c][i] & 0xffffu);
+                    o[2 * i + 1] = f16_bits_to_f32(raw[c][i] >> 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) o[j] = v[c][j];
+        }
+    };
+    // the packed words are opaque between passes, so the widened values are
+    // not kept live from one pass to the next
+    auto fence_raw = [&]() {
+        if constexpr (PACK) {
+#pragma unroll
+            for (int c = 0; c < CPT; ++c)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(raw[c][i]));
+        }
+    };
     float a = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int64_t base = (static_cast<int64_t>(c) * LANES + l) * 16;
-        if (VEC && base + 16 <= len) {
+        if constexpr (PACK) {
+            const uint16_t *xs = reinterpret_cast<const uint16_t *>(x) + off + base;
+            if (VEC && base + 16 <= len) {
+                const uint4 lo = *reinterpret_cast<const uint4 *>(xs), hi = *reinterpret_cast<const uint4 *>(xs + 8);
+                raw[c][0] = lo.x; raw[c][1] = lo.y; raw[c][2] = lo.z; raw[c][3] = lo.w;
+                raw[c][4] = hi.x; raw[c][5] = hi.y; raw[c][6] = hi.z; raw[c][7] = hi.w;
+            } else {
+                // +0 past the row's end
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t e0 = base + 2 * i < len ? xs[2 * i] : 0u;
+                    const uint32_t e1 = base + 2 * i + 1 < len ? xs[2 * i + 1] : 0u;
+                    raw[c][i] = e0 | (e1 << 16);
+                }
+            }
+        } else if (VEC && base + 16 <= len) {
             float p[8], r[8];
             load8<IN_DT>(x, off + base, p);
             load8<IN_DT>(x, off + base + 8, r);
@@ -317,8 +364,10 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
 #pragma unroll
             for (int j = 0; j < 16; ++j) v[c][j] = base + j < len ? load_scalar<IN_DT>(x, off + base + j) : 0.0f;
         }
+        float t[16];
+        get16(c, t);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) a = pmax_abs(a, v[c][j]);
+        for (int j = 0; j < 16; ++j) a = pmax_abs(a, t[j]);
     }
     // a row with NaN or infinity (NaN-propagating amax) recomputes the
     // reference's NaN-dropping amax and keeps the clamped cast; a given scale
@@ -342,26 +391,33 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
         a       = row_max(a);
         clamped = special_amax(a);
         if (clamped) {
+            fence_raw();
             a = 0.0f;
 #pragma unroll
-            for (int c = 0; c < CPT; ++c)
+            for (int c = 0; c < CPT; ++c) {
+                float t[16];
+                get16(c, t);
 #pragma unroll
-                for (int j = 0; j < 16; ++j) a = fmaxf(a, absq(v[c][j]));
+                for (int j = 0; j < 16; ++j) a = fmaxf(a, absq(t[j]));
+            }
             a = row_max(a);
         }
         sc = scale_from_amax<FMT>(a, 1e-12f);
     }
     if (l == 0) scale_inv[row] = 1.0f / sc;
+    fence_raw();
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int64_t base = (static_cast<int64_t>(c) * LANES + l) * 16;
+        float t[16];
+        get16(c, t);
         if (VEC && base + 16 <= len) {
             uint4 w;
             if (clamped) {
-                w = make_uint4(quant4<FMT>(&v[c][0], sc), quant4<FMT>(&v[c][4], sc), quant4<FMT>(&v[c][8], sc),
-                               quant4<FMT>(&v[c][12], sc));
+                w = make_uint4(quant4<FMT>(&t[0], sc), quant4<FMT>(&t[4], sc), quant4<FMT>(&t[8], sc),
+                               quant4<FMT>(&t[12], sc));
             } else {
-                const float *x = v[c];
+                const float *x = t;
                 w = make_uint4(cast4<FMT>(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc),
                                cast4<FMT>(x[4] * sc, x[5] * sc, x[6] * sc, x[7] * sc),
                                cast4<FMT>(x[8] * sc, x[9] * sc, x[10] * sc, x[11] * sc),
@@ -370,7 +426,7 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
             *reinterpret_cast<uint4 *>(q + off + base) = w;
         } else {
             for (int j = 0; j < 16; ++j)
-                if (base + j < len) q[off + base + j] = cvt1_fp8<FMT>(qclamp<FMT>(v[c][j], sc));
+                if (base + j < len) q[off + base + j] = cvt1_fp8<FMT>(qclamp<FMT>(t[j], sc));
         }
     }
 }
