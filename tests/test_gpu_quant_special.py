@@ -74,6 +74,31 @@ def test_rowwise_special(qdt):
         assert_f32_bitexact(f32(s), so, f"scales (axis {axis})")
 
 
+@pytest.mark.parametrize("width", [1040, 2064, 3088, 4096])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("qdt", FP8)
+def test_rowwise_packed_rows_special(width, dtype, qdt):
+    """Last-axis rowwise on 16-bit rows of 1040-4096 elements: the wave-per-row
+    kernel holds them packed two per register, with lanes whose 16-element
+    chunk lies past the row's end (widths that are not a multiple of 1024).
+    Rows carry NaN, +-inf, the largest finite value and NaN in the last
+    element; the others are plain N(0,1) with outliers."""
+    turbo, SG, _ = _turbo()
+    x = randn((67, width), dtype=dtype, seed=23, outliers=0.001)
+    big = torch.finfo(dtype).max
+    x[1, 5] = float("nan")
+    x[2, width - 1] = float("inf")
+    x[3, 1000] = float("-inf")
+    x[4, 7] = big
+    x[4, width - 2] = -big
+    x[5, width - 1] = float("nan")
+    x[6, :] = 0.0
+    q, s = turbo.ops.quantize_fp8(x.cuda(), qdt, SG.ROWWISE, axis=-1)
+    qo, so = O.quant_rowwise(x, FMT[qdt], -1)
+    assert_bytes_equal(u8(q), qo, "fp8 bytes")
+    assert_f32_bitexact(f32(s), so, "scales")
+
+
 @pytest.mark.parametrize("qdt", FP8)
 def test_blockwise_1d_and_dual_special(qdt):
     turbo, SG, _ = _turbo()
