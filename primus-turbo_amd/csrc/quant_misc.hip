@@ -302,10 +302,10 @@ __global__ __launch_bounds__(NT) void rw_last_kernel(const void *x, int64_t rows
     if (WAVE_PER_ROW && row >= rows) return; // whole wave exits together
     const int64_t off = row * len;
 
-    // 16-bit inputs of a vector wave-per-row launch stay packed (8 VGPRs per 16
+    // 16-bit inputs of a vector launch stay packed (8 VGPRs per 16
     // values instead of 16) and are widened again in each pass that uses
     // them: the kernel then fits 8 waves per SIMD
-    constexpr bool PACK = VEC && WAVE_PER_ROW && IN_DT != PTA_F32;
+    constexpr bool PACK = VEC && IN_DT != PTA_F32;
     float    v[PACK ? 1 : CPT][16];
     uint32_t raw[PACK ? CPT : 1][8];
     auto get16 = [&](int c, float (&o)[16]) {

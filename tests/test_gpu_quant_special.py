@@ -74,13 +74,14 @@ def test_rowwise_special(qdt):
         assert_f32_bitexact(f32(s), so, f"scales (axis {axis})")
 
 
-@pytest.mark.parametrize("width", [1040, 2064, 3088, 4096])
+@pytest.mark.parametrize("width", [1040, 2064, 3088, 4096, 6160, 14336])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("qdt", FP8)
 def test_rowwise_packed_rows_special(width, dtype, qdt):
-    """Last-axis rowwise on 16-bit rows of 1040-4096 elements: the wave-per-row
-    kernel holds them packed two per register, with lanes whose 16-element
-    chunk lies past the row's end (widths that are not a multiple of 1024).
+    """Last-axis rowwise on 16-bit rows of 1040-14336 elements: the wave-per-row
+    (up to 4096) and workgroup-per-row kernels hold them packed two per
+    register, with lanes whose 16-element chunk lies past the row's end
+    (widths that are not a multiple of the chunk span).
     Rows carry NaN, +-inf, the largest finite value and NaN in the last
     element; the others are plain N(0,1) with outliers."""
     turbo, SG, _ = _turbo()
